@@ -1,0 +1,1125 @@
+// MI355X-native RARE emulated-FP64 GEMM: HIP kernels for gfx950 and the C ABI
+// declared in include/fp64emu.h.
+//
+// Pipeline per call (one HIP stream, no host synchronisation, no allocation):
+//   1. sizing      size_rows_kernel / size_cols_* / pick_width_kernel
+//                  per-row (A) and per-column (B) power-of-two shifts, the
+//                  Cauchy-Schwarz width pick, bits_eff kept on the device.
+//   2. extraction  extract_kernel: integer-only RNE scaling of the fp64
+//                  encoding, balanced residues for every modulus and the
+//                  hi7/q7 correction operands, written directly in the
+//                  MFMA fragment order of the GEMM (tile-blocked planes).
+//   3. modgemm     modgemm_kernel: one INT8-MFMA engine over all
+//                  (slot, batch member, 256x256 tile) work items, LDS
+//                  double-buffered, XCD-aware tile order; epilogue reduces
+//                  residue slots to balanced int8 and stores correction
+//                  slots as raw int32.
+//   4. reconstruct reconstruct_kernel: balanced Garner digits with
+//                  v_dot4_i32_i8, grouped Horner, exact 128-bit combine with
+//                  the correction, correctly rounded conversion, rescale.
+//
+// The arithmetic each stage computes follows fp64_emu_cuda/fp64_emu.cu of the
+// reference (line citations at each kernel); the data layouts, launch shapes
+// and the modular reductions are this build's own.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "fp64emu.h"
+
+namespace {
+
+constexpr int kMaxP = FP64EMU_MAXP;
+constexpr int kGarnerWords = (kMaxP + 3) / 4;   // packed int8 Garner factors per row
+constexpr int kThreads = 256;
+constexpr int kTileR = 256;                      // plane tile rows (A and B alike)
+constexpr int kTileK = 64;                       // plane tile depth
+constexpr int kTileBytes = kTileR * kTileK;      // 16 KiB, one LDS stage per operand
+constexpr int kFragBytes = 1024;                 // 16 rows x 64 k in MFMA lane order
+constexpr int kOutBlkBytes = 256;                // one 16x16 int8 output block
+constexpr int kMaxSlab = 128;
+constexpr int64_t kMaxKSingle = 131071;          // int32 accumulator bound: K * 128^2 < 2^31
+constexpr int64_t kMaxKFusedCorr = 65536;        // 2K * 127^2 < 2^31: both cross GEMMs in one
+// x + kMagic (|x| < 2^51) lands on the integer grid of [2^52, 2^53): the sum
+// rounds x to the nearest integer, ties to even.
+constexpr double kMagic = 6755399441055744.0;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+// ---------------------------------------------------------------------------
+// Modulus tables, passed to the kernels by value (kernarg segment): no device
+// allocation and no host-to-device copy, so the first call is already
+// capture-safe.  Definitions follow fp64_emu_cuda/fp64_emu.cu:958-993 and
+// :1052 (reference), computed here with an extended-Euclid inverse.
+struct ModTables {
+  int P;
+  int p[kMaxP];
+  int minv[kMaxP];                 // (M_t mod p_t)^-1 mod p_t, M_t = prod_{u<t} p_u
+  int mp[kMaxP * kGarnerWords];    // balanced int8 (M_u mod p_t) for u < t, 4 per word
+  long long m64[2];                // prod of moduli 0..6 and 7..13 (1 if empty)
+  double invp[kMaxP];              // RN(1 / p)
+  double c27[kMaxP];               // 2^27 mod p
+  float log2M;                     // float sum of (float)log2(p), as the reference
+};
+
+int inv_mod(int a, int m) {
+  // Extended Euclid on (a mod m, m); m <= 256, gcd 1 by coprimality.
+  int r0 = ((a % m) + m) % m, r1 = m, s0 = 1, s1 = 0;
+  while (r1 != 0) {
+    const int q = r0 / r1;
+    int t = r0 - q * r1; r0 = r1; r1 = t;
+    t = s0 - q * s1; s0 = s1; s1 = t;
+  }
+  return ((s0 % m) + m) % m;
+}
+
+int gcd_int(int a, int b) {
+  while (b) { const int t = a % b; a = b; b = t; }
+  return a;
+}
+
+ModTables make_tables(const int32_t* primes, int P) {
+  ModTables T;
+  std::memset(&T, 0, sizeof(T));
+  T.P = P;
+  for (int g = 0; g < 2; ++g) {
+    long long prod = 1;
+    for (int t = 7 * g; t < std::min(7 * g + 7, P); ++t) prod *= primes[t];
+    T.m64[g] = prod;
+  }
+  float l2 = 0.0f;
+  for (int t = 0; t < P; ++t) {
+    const int pt = primes[t];
+    T.p[t] = pt;
+    T.invp[t] = 1.0 / (double)pt;
+    T.c27[t] = (double)((1LL << 27) % pt);
+    l2 += (float)std::log2((double)pt);
+    long long Mu = 1 % pt;   // M_u mod p_t, running over u
+    for (int u = 0; u < t; ++u) {
+      int bal = (int)Mu;
+      if (bal > (pt - 1) / 2) bal -= pt;
+      T.mp[t * kGarnerWords + (u >> 2)] |= (int)((uint32_t)(uint8_t)(int8_t)bal << (8 * (u & 3)));
+      Mu = (Mu * (primes[u] % pt)) % pt;
+    }
+    T.minv[t] = inv_mod((int)Mu, pt);
+  }
+  T.log2M = l2;
+  return T;
+}
+
+// ---------------------------------------------------------------------------
+// Workspace map.
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+// Column-sizing slab split of a [K, N] operand; the same split as
+// fp64_emu_cuda/fp64_emu.cu:1159-1162 so the fp64 sum order matches.
+void slab_split(int64_t NF, int64_t K, int64_t* kslab, int* nslab) {
+  if (K <= 0 || NF <= 0) { *kslab = 0; *nslab = 0; return; }
+  const int64_t nsl0 = std::min<int64_t>(std::max<int64_t>(131072 / NF, 1), kMaxSlab);
+  *kslab = (K + nsl0 - 1) / nsl0;
+  *nslab = (int)((K + *kslab - 1) / *kslab);
+}
+
+void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool corr,
+                 fp64emu_layout_t* L) {
+  std::memset(L, 0, sizeof(*L));
+  L->batch = batch; L->M = M; L->N = N; L->K = K;
+  L->nprimes = P; L->use_corr = corr ? 1 : 0;
+  L->ncorr = corr ? (K <= kMaxKFusedCorr ? 1 : 2) : 0;
+  int64_t kslab; int nslab;
+  slab_split(batch * N, K, &kslab, &nslab);
+  L->nslab = nslab;
+  L->Mp = round_up(std::max<int64_t>(M, 1), kTileR);
+  L->Np = round_up(std::max<int64_t>(N, 1), kTileR);
+  L->Kp = round_up(K, kTileK);
+  L->planeA_bytes = L->Mp * L->Kp;
+  L->planeB_bytes = L->Np * L->Kp;
+  const int nplanes = P + (corr ? 2 : 0);   // the correction plane is 2*Kp deep
+  L->memberA_bytes = (int64_t)nplanes * L->planeA_bytes;
+  L->memberB_bytes = (int64_t)nplanes * L->planeB_bytes;
+  L->outplane_bytes = L->Mp * L->Np;
+  size_t o = 0;
+  auto take = [&](size_t bytes) { const size_t at = o; o = align_up(o + bytes); return at; };
+  L->off_sftA = take(sizeof(int16_t) * batch * M);
+  L->off_sftB = take(sizeof(int16_t) * batch * N);
+  L->off_lgA = take(sizeof(float) * batch * M);
+  L->off_lgB = take(sizeof(float) * batch * N);
+  L->off_bits = take(sizeof(int) * 4);
+  L->off_pmax = take(sizeof(double) * (size_t)nslab * batch * N);
+  L->off_pss = take(sizeof(double) * (size_t)nslab * batch * N);
+  L->off_planesA = take((size_t)(batch * L->memberA_bytes));
+  L->off_planesB = take((size_t)(batch * L->memberB_bytes));
+  L->off_res8 = take((size_t)(batch * P * L->outplane_bytes));
+  L->off_corr = take(sizeof(int32_t) * (size_t)(batch * L->ncorr * L->outplane_bytes));
+  L->total = o;
+}
+
+// ---------------------------------------------------------------------------
+// Sizing.  Per row: max|x| and the fp64 sum of squares with the reference's
+// order (thread-strided partial sums, FMA accumulate, 256-wide tree), so the
+// Cauchy-Schwarz decision is reproducible by the CPU restatement.
+// fp64_emu_cuda/fp64_emu.cu:107-146.
+__device__ __forceinline__ void row_stats_out(double m, double s2, int bits, int16_t* sft,
+                                              float* lg) {
+  const int e = (m > 0.0 && isfinite(m)) ? ilogb(m) : 0;
+  const int sh = (bits - 1) - e;
+  float l;
+  if (s2 > 0.0 && isfinite(s2)) l = (float)(0.5 * log2(s2) + (double)sh);
+  else l = (m > 0.0) ? INFINITY : -INFINITY;
+  *lg = l;
+  *sft = (int16_t)sh;
+}
+
+__global__ void __launch_bounds__(kThreads)
+size_rows_kernel(const double* __restrict__ A, int64_t rowsA, const double* __restrict__ B,
+                 int64_t K, int bits, int16_t* __restrict__ sftA, float* __restrict__ lgA,
+                 int16_t* __restrict__ sftB, float* __restrict__ lgB) {
+  const int64_t br = blockIdx.x;
+  const bool isA = br < rowsA;
+  const int64_t r = isA ? br : br - rowsA;
+  const double* __restrict__ x = (isA ? A : B) + r * K;
+  const int tid = threadIdx.x;
+  double mx = 0.0, ss = 0.0;
+  for (int64_t c = tid; c < K; c += kThreads) {
+    const double v = x[c];
+    mx = fmax(mx, fabs(v));
+    ss = fma(v, v, ss);
+  }
+  __shared__ double smx[kThreads], sss[kThreads];
+  smx[tid] = mx;
+  sss[tid] = ss;
+  __syncthreads();
+#pragma unroll
+  for (int s = kThreads / 2; s > 0; s >>= 1) {
+    if (tid < s) {
+      smx[tid] = fmax(smx[tid], smx[tid + s]);
+      sss[tid] = sss[tid] + sss[tid + s];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    if (isA) row_stats_out(smx[0], sss[0], bits, &sftA[r], &lgA[r]);
+    else row_stats_out(smx[0], sss[0], bits, &sftB[r], &lgB[r]);
+  }
+}
+
+// Column partials of a [K, N] operand (per batch member): thread j owns
+// global column j, blockIdx.y a k-slab summed in order.
+// fp64_emu_cuda/fp64_emu.cu:148-169.
+__global__ void __launch_bounds__(kThreads)
+size_cols_partial_kernel(const double* __restrict__ X, int64_t totalcols, int64_t rows_per,
+                         int64_t cols_per, int64_t kslab, double* __restrict__ pmax,
+                         double* __restrict__ pss) {
+  const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (j >= totalcols) return;
+  const int64_t b = j / cols_per, n = j - b * cols_per;
+  const int64_t k0 = (int64_t)blockIdx.y * kslab;
+  const int64_t k1 = min(k0 + kslab, rows_per);
+  const double* __restrict__ base = X + b * rows_per * cols_per + n;
+  double mx = 0.0, ss = 0.0;
+  for (int64_t k = k0; k < k1; ++k) {
+    const double v = base[k * cols_per];
+    mx = fmax(mx, fabs(v));
+    ss = fma(v, v, ss);
+  }
+  pmax[(int64_t)blockIdx.y * totalcols + j] = mx;
+  pss[(int64_t)blockIdx.y * totalcols + j] = ss;
+}
+
+// Slabs folded in order.  fp64_emu_cuda/fp64_emu.cu:171-189.
+__global__ void __launch_bounds__(kThreads)
+size_cols_final_kernel(const double* __restrict__ pmax, const double* __restrict__ pss,
+                       int64_t totalcols, int nslab, int bits, int16_t* __restrict__ sft,
+                       float* __restrict__ lg) {
+  const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (j >= totalcols) return;
+  double mx = 0.0, ss = 0.0;
+  for (int s = 0; s < nslab; ++s) {
+    mx = fmax(mx, pmax[(int64_t)s * totalcols + j]);
+    ss = ss + pss[(int64_t)s * totalcols + j];
+  }
+  row_stats_out(mx, ss, bits, &sft[j], &lg[j]);
+}
+
+// Width pick: g = floor((log2M - 1 - (max lgA + max lgB + 0.5)) / 2),
+// g <= 53 - bits, be = max(bits + g, 16); g folded into every shift and be
+// kept on the device.  fp64_emu_cuda/fp64_emu.cu:191-231.
+__global__ void __launch_bounds__(kThreads)
+pick_width_kernel(const float* __restrict__ lgA, int64_t m, const float* __restrict__ lgB,
+                  int64_t n, float log2M, int bits, int16_t* __restrict__ sftA,
+                  int16_t* __restrict__ sftB, int* __restrict__ bits_eff) {
+  __shared__ float sa[kThreads], sb[kThreads];
+  __shared__ int s_g;
+  const int tid = threadIdx.x;
+  float a = -INFINITY, b = -INFINITY;
+  for (int64_t i = tid; i < m; i += kThreads) a = fmaxf(a, lgA[i]);
+  for (int64_t j = tid; j < n; j += kThreads) b = fmaxf(b, lgB[j]);
+  sa[tid] = a;
+  sb[tid] = b;
+  __syncthreads();
+  for (int s = kThreads / 2; s > 0; s >>= 1) {
+    if (tid < s) {
+      sa[tid] = fmaxf(sa[tid], sa[tid + s]);
+      sb[tid] = fmaxf(sb[tid], sb[tid + s]);
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const float need = sa[0] + sb[0] + 0.5f;
+    int g = 0;
+    if (isfinite(need)) g = (int)floorf((log2M - 1.0f - need) * 0.5f);
+    g = min(g, 53 - bits);
+    const int be = max(bits + g, 16);
+    s_g = be - bits;
+    bits_eff[0] = be;
+  }
+  __syncthreads();
+  const int g = s_g;
+  if (g != 0) {
+    for (int64_t i = tid; i < m; i += kThreads) sftA[i] = (int16_t)(sftA[i] + g);
+    for (int64_t j = tid; j < n; j += kThreads) sftB[j] = (int16_t)(sftB[j] + g);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Extraction.  Element semantics follow fp64_emu_cuda/fp64_emu.cu:288-321
+// (integer-only RNE scaling of the IEEE encoding, hi7/q7 correction
+// summaries); the residue reduction is this build's: the signed integer
+// td = +-round(|x| 2^s) splits as th * 2^27 + tl (th signed, tl < 2^27),
+// v = th * (2^27 mod p) + tl is exact in fp64 (|v| < 2^35), and
+// r = v - p * RNE(v / p) is exact: the quotient error (< 2^-26) stays far
+// below the distance 1/(2p) of v/p from a half-integer for odd p, and 1/256
+// is exact.  r is the balanced residue; p = 256 may give +128, whose byte is
+// the reference's -128.
+//
+// Plane layout (per batch member, per plane): 256-row x 64-k tiles, row tile
+// major, k tile minor; inside a tile, 16 fragments of 16 rows, each 1 KiB in
+// MFMA lane order: lane l = 16 * (k / 16) + (row % 16) holds k % 16 in its
+// 16 bytes.  The correction plane is one 2*Kp-deep plane: A = [hi7 | q7],
+// B = [q7 | hi7], so one GEMM accumulates hi7_A q7_B^T + q7_A hi7_B^T.
+
+__device__ __forceinline__ uint64_t rne_shift_right(uint64_t mag, int s) {
+  if (s <= 0) return (s > -64) ? (mag << (-s)) : 0ull;
+  if (s > 63) return 0ull;
+  const uint64_t kept = mag >> s;
+  const uint64_t dropped = mag - (kept << s);
+  const uint64_t half = 1ull << (s - 1);
+  const bool up = (dropped > half) || (dropped == half && (kept & 1ull));
+  return kept + (up ? 1ull : 0ull);
+}
+
+struct ExtractArgs {
+  const double* A;
+  const double* B;
+  int64_t M, N, K, batch;
+  int b_kn;          // B given as [K, N] (mm_nt / bmm_nt)
+  int use_corr;
+  int64_t nkt;       // Kp / 64
+  int64_t planeA, planeB, memberA, memberB;
+  int64_t wgA;       // work groups of the A part; B follows
+  int64_t rgA, rgB;  // 64-row groups per member: Mp / 64, Np / 64
+  const int16_t* sftA;
+  const int16_t* sftB;
+  const int* bits_eff;
+  int8_t* planesA;
+  int8_t* planesB;
+  ModTables tab;
+};
+
+__global__ void __launch_bounds__(kThreads)
+extract_kernel(ExtractArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int64_t wg = blockIdx.x;
+  const bool isA = wg < a.wgA;
+  if (!isA) wg -= a.wgA;
+  const bool kn = !isA && a.b_kn;
+  // Work group -> (member, 64-row group, k tile).  Row-major operands walk k
+  // fastest (consecutive groups read consecutive bytes of the same rows);
+  // the [K, N] operand walks the 64-column group fastest.
+  const int64_t rg_per = isA ? a.rgA : a.rgB;
+  int64_t b, rg, kt;
+  if (kn) {
+    rg = wg % rg_per;
+    const int64_t t = wg / rg_per;
+    kt = t % a.nkt;
+    b = t / a.nkt;
+  } else {
+    kt = wg % a.nkt;
+    const int64_t t = wg / a.nkt;
+    rg = t % rg_per;
+    b = t / rg_per;
+  }
+  const int64_t R = isA ? a.M : a.N;
+  const int64_t K = a.K;
+  const int64_t rblk = rg * 4 + wave;                // 16-row fragment index
+  const int64_t r = rblk * 16 + (lane & 15);         // plane row (A row or B column)
+  const int64_t k0 = kt * kTileK + (lane >> 4) * 16; // first of this lane's 16 k
+  const bool rowok = r < R;
+
+  // Shift: per row of A / of B [N,K]; per column of B [K,N] -- one per lane.
+  const int16_t* sfts = isA ? a.sftA : a.sftB;
+  const int shift = rowok ? (int)sfts[b * R + r] : 0;
+  const int be = a.bits_eff[0];
+
+  double x[16];
+  if (!rowok || k0 >= K) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) x[j] = 0.0;
+  } else if (kn) {
+    const double* __restrict__ src = a.B + (b * K + k0) * a.N + r;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) x[j] = (k0 + j < K) ? src[(int64_t)j * a.N] : 0.0;
+  } else {
+    const double* __restrict__ src = (isA ? a.A : a.B) + (b * R + r) * K + k0;
+    if (k0 + 16 <= K) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) x[j] = src[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) x[j] = (k0 + j < K) ? src[j] : 0.0;
+    }
+  }
+
+  // Split every element first: th, tl as exact doubles, hi7/q7 bytes.
+  double th[16], tl[16];
+  uint32_t hw[4] = {0u, 0u, 0u, 0u}, qw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int jj = 0; jj < 16; ++jj) {
+    const uint64_t xb = (uint64_t)__double_as_longlong(x[jj]);
+    const bool neg = (xb >> 63) != 0;
+    const int e = (int)((xb >> 52) & 0x7FF);
+    const uint64_t mant = xb & 0xFFFFFFFFFFFFFull;
+    const uint64_t mag = e ? (mant | (1ull << 52)) : mant;
+    // |x| * 2^shift = mag * 2^(t - 52); subnormals read as exponent 1.
+    const int t = (e ? e : 1) - 1075 + shift + 52;
+    const uint64_t Tu = rne_shift_right(mag, 52 - t);
+    const int64_t td = neg ? -(int64_t)Tu : (int64_t)Tu;
+    if (a.use_corr) {
+      const int64_t r8 = (int64_t)rne_shift_right(mag, 44 - t) - (int64_t)(Tu << 8);
+      const int64_t h8 = (int64_t)rne_shift_right(Tu, be - 7);
+      int64_t hs = neg ? -h8 : h8, qs = neg ? -r8 : r8;
+      hs = hs > 127 ? 127 : (hs < -127 ? -127 : hs);
+      qs = qs > 127 ? 127 : (qs < -127 ? -127 : qs);
+      hw[jj >> 2] |= ((uint32_t)hs & 0xFFu) << (8 * (jj & 3));
+      qw[jj >> 2] |= ((uint32_t)qs & 0xFFu) << (8 * (jj & 3));
+    }
+    const int64_t hi = td >> 27;                   // arithmetic: floor(td / 2^27)
+    th[jj] = (double)hi;
+    tl[jj] = (double)(td - (hi << 27));            // in [0, 2^27)
+  }
+
+  // One plane at a time: 16 residues -> one 16-byte chunk per lane, 1 KiB
+  // contiguous per wave.
+  const int P = a.tab.P;
+  const int64_t nkt = a.nkt;
+  const int64_t rt = rblk >> 4, fr = rblk & 15;
+  const int64_t plane = isA ? a.planeA : a.planeB;
+  int8_t* base = (isA ? a.planesA : a.planesB) + b * (isA ? a.memberA : a.memberB);
+  const int64_t off = (rt * nkt + kt) * kTileBytes + fr * kFragBytes + lane * 16;
+  for (int pi = 0; pi < P; ++pi) {
+    const double pd = (double)a.tab.p[pi], ip = a.tab.invp[pi], c27 = a.tab.c27[pi];
+    uint32_t w4[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint32_t w = 0u;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const double v = fma(th[4 * g + u], c27, tl[4 * g + u]);
+        const double q = fma(v, ip, kMagic) - kMagic;
+        const int rr = (int)fma(-q, pd, v);
+        w |= ((uint32_t)rr & 0xFFu) << (8 * u);
+      }
+      w4[g] = w;
+    }
+    *reinterpret_cast<v4i*>(base + pi * plane + off) =
+        v4i{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
+  }
+  if (a.use_corr) {
+    // Correction plane: row tile stride 2*nkt tiles; A = [hi | q], B = [q | hi].
+    int8_t* cb = base + (int64_t)P * plane;
+    const int64_t o1 = (rt * 2 * nkt + kt) * kTileBytes + fr * kFragBytes + lane * 16;
+    const int64_t o2 = o1 + nkt * kTileBytes;
+    const v4i hv = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
+    const v4i qv = v4i{(int)qw[0], (int)qw[1], (int)qw[2], (int)qw[3]};
+    *reinterpret_cast<v4i*>(cb + o1) = isA ? hv : qv;
+    *reinterpret_cast<v4i*>(cb + o2) = isA ? qv : hv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Modular GEMM engine.  Work item = (slot, batch member, 256x256 output tile);
+// slot = correction GEMM(s) first (they are twice as deep), then one slot per
+// modulus.  Exact int32 C = A_plane B_plane^T per slot
+// (fp64_emu_cuda/fp64_emu.cu:491-657); epilogue: balanced int8 residue for
+// modulus slots (the reference's bal8, :613-620, here as an exact fp64
+// nearest-quotient reduction), raw int32 for correction slots.
+//
+// 4 waves in a 2x2 arrangement, 128x128 per wave = 8x8 MFMA 16x16x64 tiles
+// (256 accumulator registers), LDS double-buffered 32 KiB stages fed by
+// coalesced 16-byte loads of the fragment-ordered planes; fragment reads are
+// linear 16 B per lane, so they are bank-conflict free.
+//
+// Output blocks (res8 / corr planes): 16x16 blocks, row-block major; inside
+// a block lane l = 16 * (row / 4) + col holds rows 4*(l/16) + 0..3 of column
+// l % 16 -- the MFMA accumulator order -- as 4 consecutive bytes (int8) or
+// 4 consecutive int32.
+
+struct GemmArgs {
+  const int8_t* A;
+  const int8_t* B;
+  int8_t* res8;
+  int32_t* corr;
+  int64_t memberA, memberB, planeA, planeB;
+  int64_t outplane;    // Mp * Np
+  int64_t total;       // work groups
+  int nkt;             // k tiles of a residue plane
+  int TM, TN;          // 256-tiles per member
+  int P, ncorr, nslots, batch;
+  int p[kMaxP];
+  double invp[kMaxP];
+};
+
+__global__ void __launch_bounds__(kThreads, 1)
+modgemm_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) int8_t lds[2][2 * kTileBytes];
+
+  // XCD-aware order: work group i runs on XCD i % 8.  Within each full chunk
+  // of 256 groups, XCD x takes logical items 32x .. 32x+31, an 8x4 block of
+  // tiles sharing 12 operand panels in that XCD's L2, while all XCDs work on
+  // the same slot (whose planes then stay resident in the MALL).
+  const int64_t i = blockIdx.x;
+  int64_t L = i;
+  if ((i >> 8) < (g.total >> 8)) L = (i & ~255ll) + (i & 7) * 32 + ((i & 255) >> 3);
+  const int64_t tiles = (int64_t)g.TM * g.TN;
+  const int64_t sb = L / tiles;
+  const int tile = (int)(L - sb * tiles);
+  const int slot = (int)(sb / g.batch);
+  const int64_t b = sb - (int64_t)slot * g.batch;
+  // Grouped tile order: 8 row tiles per group, column-major inside.
+  const int GM = 8;
+  const int grp = tile / (GM * g.TN);
+  const int first_m = grp * GM;
+  const int gm = min(g.TM - first_m, GM);
+  const int within = tile - grp * GM * g.TN;
+  const int mt = first_m + within % gm;
+  const int nt = within / gm;
+
+  // Slot -> operand plane, k-tile window and output.
+  const bool is_corr = slot < g.ncorr;
+  const int plane = is_corr ? g.P : slot - g.ncorr;
+  const int rstride = is_corr ? 2 * g.nkt : g.nkt;           // k tiles per row tile
+  const int kt0 = (is_corr && g.ncorr == 2) ? slot * g.nkt : 0;
+  const int nk = is_corr ? (g.ncorr == 1 ? 2 * g.nkt : g.nkt) : g.nkt;
+
+  const v4i* __restrict__ At = reinterpret_cast<const v4i*>(
+      g.A + b * g.memberA + (int64_t)plane * g.planeA + ((int64_t)mt * rstride + kt0) * kTileBytes);
+  const v4i* __restrict__ Bt = reinterpret_cast<const v4i*>(
+      g.B + b * g.memberB + (int64_t)plane * g.planeB + ((int64_t)nt * rstride + kt0) * kTileBytes);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  constexpr int kV = kTileBytes / 16;   // v4i per operand tile (1024)
+
+  v4i acc[8][8];
+#pragma unroll
+  for (int x = 0; x < 8; ++x)
+#pragma unroll
+    for (int y = 0; y < 8; ++y) acc[x][y] = v4i{0, 0, 0, 0};
+
+  v4i ra[4], rb[4];
+  if (nk > 0) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      ra[u] = At[u * kThreads + tid];
+      rb[u] = Bt[u * kThreads + tid];
+    }
+    v4i* s0 = reinterpret_cast<v4i*>(lds[0]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      s0[u * kThreads + tid] = ra[u];
+      s0[kV + u * kThreads + tid] = rb[u];
+    }
+  }
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const bool more = kt + 1 < nk;
+    if (more) {
+      const v4i* an = At + (int64_t)(kt + 1) * kV;
+      const v4i* bn = Bt + (int64_t)(kt + 1) * kV;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        ra[u] = an[u * kThreads + tid];
+        rb[u] = bn[u * kThreads + tid];
+      }
+    }
+    const v4i* sa = reinterpret_cast<const v4i*>(lds[kt & 1]);
+    const v4i* sbp = sa + kV;
+    v4i af[8], bf[8];
+#pragma unroll
+    for (int x = 0; x < 8; ++x) af[x] = sa[(wm * 8 + x) * 64 + lane];
+#pragma unroll
+    for (int y = 0; y < 8; ++y) bf[y] = sbp[(wn * 8 + y) * 64 + lane];
+#pragma unroll
+    for (int x = 0; x < 8; ++x)
+#pragma unroll
+      for (int y = 0; y < 8; ++y)
+        acc[x][y] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[x], bf[y], acc[x][y], 0, 0, 0);
+    if (more) {
+      v4i* sn = reinterpret_cast<v4i*>(lds[(kt + 1) & 1]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        sn[u * kThreads + tid] = ra[u];
+        sn[kV + u * kThreads + tid] = rb[u];
+      }
+    }
+    __syncthreads();
+  }
+
+  // Epilogue.
+  const int64_t NB = (int64_t)g.TN * 16;              // 16-blocks per output row
+  const int64_t mb0 = (int64_t)mt * 16 + wm * 8, nb0 = (int64_t)nt * 16 + wn * 8;
+  if (is_corr) {
+    int32_t* dst = g.corr + (b * g.ncorr + slot) * g.outplane;
+#pragma unroll
+    for (int x = 0; x < 8; ++x)
+#pragma unroll
+      for (int y = 0; y < 8; ++y)
+        *reinterpret_cast<v4i*>(dst + ((mb0 + x) * NB + nb0 + y) * kOutBlkBytes + lane * 4) =
+            acc[x][y];
+  } else {
+    const int t = plane;
+    const double pd = (double)g.p[t], ip = g.invp[t];
+    int8_t* dst = g.res8 + (b * g.P + t) * g.outplane;
+#pragma unroll
+    for (int x = 0; x < 8; ++x)
+#pragma unroll
+      for (int y = 0; y < 8; ++y) {
+        uint32_t w = 0u;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          // |acc| < 2^31: the nearest quotient is exact (see extraction).
+          const double av = (double)acc[x][y][v];
+          const double q = fma(av, ip, kMagic) - kMagic;
+          const int rr = (int)fma(-q, pd, av);
+          w |= ((uint32_t)rr & 0xFFu) << (8 * v);
+        }
+        *reinterpret_cast<uint32_t*>(dst + ((mb0 + x) * NB + nb0 + y) * kOutBlkBytes + lane * 4) = w;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Reconstruction.  Per output element: balanced Garner digits
+//   d_t = bal((r_t - sum_{u<t} d_u (M_u mod p_t)) (M_t mod p_t)^-1 mod p_t)
+// with the O(P^2) inner products as v_dot4_i32_i8 over packed digits; int64
+// Horner per group of 7 moduli; exact: 128-bit a0 + M0 (a1 + M1 a2) plus the
+// correction (corr1 + corr2) << (be - 15), correctly rounded to double, then
+// ldexp by -(sftA + sftB).  fp64_emu_cuda/fp64_emu.cu:849-952 and the s128
+// helpers :53-105.  One wave per 16x16 output block, 4 elements per lane.
+
+struct s128v {
+  uint64_t lo;
+  int64_t hi;
+};
+
+__device__ __forceinline__ s128v s128_of(int64_t v) {
+  return s128v{(uint64_t)v, v < 0 ? -1ll : 0ll};
+}
+
+// a * m + d, m < 2^57 positive, d signed 64-bit; exact while |a*m| < 2^126.
+__device__ __forceinline__ s128v s128_fma64(s128v a, uint64_t m, int64_t d) {
+  const uint64_t lo = a.lo * m;
+  const int64_t hi = (int64_t)__umul64hi(a.lo, m) + a.hi * (int64_t)m;
+  s128v r;
+  r.lo = lo + (uint64_t)d;
+  r.hi = hi + (r.lo < lo ? 1 : 0) + (d < 0 ? -1 : 0);
+  return r;
+}
+
+__device__ __forceinline__ s128v s128_add_shl(s128v a, int64_t c, int s) {
+  // a + c * 2^s for 0 < s < 64.
+  const uint64_t clo = (uint64_t)c << s;
+  const int64_t chi = (int64_t)(((uint64_t)(c < 0 ? -1ll : 0ll) << s) | ((uint64_t)c >> (64 - s)));
+  s128v r;
+  r.lo = a.lo + clo;
+  r.hi = a.hi + chi + (r.lo < clo ? 1 : 0);
+  return r;
+}
+
+// Round-to-nearest-even conversion of a signed 128-bit integer: the top 64
+// significant bits with the dropped tail as a sticky bit (11 positions below
+// the rounding point) convert once.
+__device__ __forceinline__ double s128_to_f64(s128v a) {
+  const bool neg = a.hi < 0;
+  uint64_t lo = a.lo, hi = (uint64_t)a.hi;
+  if (neg) {
+    lo = ~lo + 1ull;
+    hi = ~hi + (lo == 0ull ? 1ull : 0ull);
+  }
+  double m;
+  if (hi == 0ull) {
+    m = (double)lo;
+  } else {
+    const int s = 64 - __clzll((long long)hi);      // 1..64 bits above the low word
+    uint64_t top, tail;
+    if (s == 64) { top = hi; tail = lo; }
+    else { top = (hi << (64 - s)) | (lo >> s); tail = lo << (64 - s); }
+    m = ldexp((double)(top | (tail != 0ull ? 1ull : 0ull)), s);
+  }
+  return neg ? -m : m;
+}
+
+struct ReconArgs {
+  const int8_t* res8;
+  const int32_t* corr;
+  double* out;
+  const int16_t* sftA;
+  const int16_t* sftB;
+  const int* bits_eff;
+  int64_t M, N, batch, outplane;
+  int64_t NB;          // 16-blocks per padded output row (Np / 16)
+  int64_t MBv, NBv;    // 16-blocks covering the valid M, N
+  int64_t nblocks;     // batch * MBv * NBv
+  int ncorr;
+  ModTables tab;
+};
+
+template <bool kExact>
+__global__ void __launch_bounds__(kThreads)
+reconstruct_kernel(ReconArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wv = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (wv >= a.nblocks) return;
+  const int64_t per = a.MBv * a.NBv;
+  const int64_t b = wv / per;
+  const int64_t rem = wv - b * per;
+  const int64_t mb = rem / a.NBv, nb = rem - (rem / a.NBv) * a.NBv;
+  const int64_t i0 = mb * 16 + 4 * (lane >> 4);
+  const int64_t j = nb * 16 + (lane & 15);
+  if (j >= a.N || i0 >= a.M) return;
+
+  const int P = a.tab.P;
+  const int64_t boff = (mb * a.NB + nb) * kOutBlkBytes + lane * 4;
+  uint32_t w[kMaxP];
+#pragma unroll
+  for (int t = 0; t < kMaxP; ++t) {
+    if (t >= P) break;
+    w[t] = *reinterpret_cast<const uint32_t*>(a.res8 + (b * P + t) * a.outplane + boff);
+  }
+  int64_t cv[4] = {0, 0, 0, 0};
+  if (a.ncorr > 0) {
+    const v4i c1 = *reinterpret_cast<const v4i*>(a.corr + (b * a.ncorr) * a.outplane + boff);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) cv[v] = c1[v];
+    if (a.ncorr == 2) {
+      const v4i c2 = *reinterpret_cast<const v4i*>(a.corr + (b * a.ncorr + 1) * a.outplane + boff);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) cv[v] += c2[v];
+    }
+  }
+  const int cshift = a.bits_eff[0] - 15;
+  const int sj = (int)a.sftB[b * a.N + j];
+  const int ng = (P + 6) / 7;
+
+  for (int v = 0; v < 4; ++v) {
+    const int64_t i = i0 + v;
+    if (i >= a.M) break;
+    int dp[kGarnerWords] = {0, 0, 0, 0, 0};
+    int dg[kMaxP];
+#pragma unroll
+    for (int t = 0; t < kMaxP; ++t) {
+      if (t >= P) continue;
+      const int rt = (int)(int8_t)(uint8_t)(w[t] >> (8 * v));
+      int d;
+      if (t == 0) {
+        d = rt;   // M_0 = 1: the first digit is the (balanced) residue
+      } else {
+        int acc = 0;
+#pragma unroll
+        for (int gw = 0; gw < kGarnerWords; ++gw)
+          if (4 * gw < t) acc = __builtin_amdgcn_sdot4(dp[gw], a.tab.mp[t * kGarnerWords + gw], acc, false);
+        const int y = (rt - acc) * a.tab.minv[t];      // |y| < 2^27
+        const double yd = (double)y;
+        const double q = fma(yd, a.tab.invp[t], kMagic) - kMagic;
+        d = (int)fma(-q, (double)a.tab.p[t], yd);
+        // Even modulus: the nearest quotient can leave +p/2; balanced is -p/2.
+        if ((a.tab.p[t] & 1) == 0 && d == a.tab.p[t] / 2) d -= a.tab.p[t];
+      }
+      dg[t] = d;
+      dp[t >> 2] |= (int)(((uint32_t)d & 0xFFu) << (8 * (t & 3)));
+    }
+    long long a0 = 0, a1 = 0, a2 = 0;
+#pragma unroll
+    for (int t = kMaxP - 1; t >= 0; --t) {
+      if (t >= P) continue;
+      const long long d = dg[t];
+      if (t >= 14) a2 = a2 * a.tab.p[t] + d;
+      else if (t >= 7) a1 = a1 * a.tab.p[t] + d;
+      else a0 = a0 * a.tab.p[t] + d;
+    }
+    const int sh = -((int)a.sftA[b * a.M + i] + sj);
+    double val;
+    if (kExact) {
+      s128v acc = s128_of(ng == 3 ? a2 : (ng == 2 ? a1 : a0));
+      if (ng == 3) acc = s128_fma64(acc, (uint64_t)a.tab.m64[1], a1);
+      if (ng >= 2) acc = s128_fma64(acc, (uint64_t)a.tab.m64[0], a0);
+      if (cv[v] != 0) acc = s128_add_shl(acc, cv[v], cshift);
+      val = s128_to_f64(acc);
+    } else {
+      double acc = (double)(ng == 3 ? a2 : (ng == 2 ? a1 : a0));
+      if (ng == 3) acc = fma(acc, (double)a.tab.m64[1], (double)a1);
+      if (ng >= 2) acc = fma(acc, (double)a.tab.m64[0], (double)a0);
+      acc = acc + ldexp((double)cv[v], cshift);
+      val = acc;
+    }
+    a.out[(b * a.M + i) * a.N + j] = ldexp(val, sh);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Double-double GEMM for correct-bits measurement (not on the product path):
+// per k, the exact product p + e (FMA error-free transform) joins hi by a
+// two-sum, the tails collect in lo, and hi/lo renormalise -- the sequence of
+// bench/accuracy.py:39-50 of the reference.  16x16 threads per block, 16x16
+// operand tiles through LDS.
+__device__ __forceinline__ void two_sum(double a, double b, double& s, double& e) {
+  s = a + b;
+  const double bb = s - a;
+  e = (a - (s - bb)) + (b - bb);
+}
+
+__global__ void __launch_bounds__(kThreads)
+ddgemm_nt_kernel(double* __restrict__ hi, double* __restrict__ lo, const double* __restrict__ A,
+                 const double* __restrict__ B, int64_t M, int64_t N, int64_t K) {
+  __shared__ double sa[16][17], sb[16][17];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int64_t i = (int64_t)blockIdx.y * 16 + ty, j = (int64_t)blockIdx.x * 16 + tx;
+  double h = 0.0, l = 0.0;
+  for (int64_t k0 = 0; k0 < K; k0 += 16) {
+    const int64_t ra = (int64_t)blockIdx.y * 16 + ty, rb = (int64_t)blockIdx.x * 16 + ty;
+    sa[ty][tx] = (ra < M && k0 + tx < K) ? A[ra * K + k0 + tx] : 0.0;
+    sb[ty][tx] = (rb < N && k0 + tx < K) ? B[rb * K + k0 + tx] : 0.0;
+    __syncthreads();
+    const int kk = (int)min<int64_t>(16, K - k0);
+    for (int k = 0; k < kk; ++k) {
+      const double x = sa[ty][k], y = sb[tx][k];
+      const double p = x * y;
+      const double e = fma(x, y, -p);
+      double s, t;
+      two_sum(h, p, s, t);
+      l = l + (t + e);
+      two_sum(s, l, h, l);
+    }
+    __syncthreads();
+  }
+  if (i < M && j < N) {
+    hi[i * N + j] = h;
+    lo[i * N + j] = l;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host orchestration.  fp64_emu_cuda/fp64_emu.cu:1127-1186, 1220-1270,
+// 1343-1407 (the fused slice): sizing -> extraction -> modular GEMMs ->
+// reconstruction on one stream, phase events when requested.
+
+struct Call {
+  double* out;
+  const double* A;
+  const double* B;
+  int64_t batch, M, N, K;
+  bool b_kn;
+  const int32_t* primes;
+  int P;
+  bool exact;
+  int bits;
+  bool corr;
+  void* ws;
+  size_t ws_bytes;
+  hipStream_t stream;
+  hipEvent_t* ev;   // 5 events or nullptr
+};
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return FP64EMU_OK;
+  return fail(FP64EMU_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int validate_primes(const int32_t* primes, int P) {
+  if (P < 1) return fail(FP64EMU_EINVAL, "nprimes must be >= 1");
+  if (P > kMaxP) return fail(FP64EMU_EINVAL, "too many primes");
+  if (!primes) return fail(FP64EMU_EINVAL, "primes must not be NULL");
+  for (int t = 0; t < P; ++t) {
+    if (primes[t] < 2 || primes[t] > 256) return fail(FP64EMU_EINVAL, "moduli must be in [2, 256]");
+    for (int u = 0; u < t; ++u)
+      if (gcd_int(primes[t], primes[u]) != 1)
+        return fail(FP64EMU_EINVAL, "moduli must be pairwise coprime");
+  }
+  return FP64EMU_OK;
+}
+
+int run(const Call& c) {
+  if (int st = validate_primes(c.primes, c.P)) return st;
+  if (c.bits < 16 || c.bits > 53) return fail(FP64EMU_EINVAL, "bits must be in [16, 53]");
+  if (c.batch < 0 || c.M < 0 || c.N < 0 || c.K < 0)
+    return fail(FP64EMU_EINVAL, "shapes must be non-negative");
+  if (c.K > kMaxKSingle) return fail(FP64EMU_EINVAL, "K bound for int32 modular GEMM");
+  fp64emu_layout_t L;
+  make_layout(c.batch, c.M, c.N, c.K, c.P, c.corr, &L);
+  const hipStream_t s = c.stream;
+  if (c.ev) {
+    if (int st = check_hip(hipEventRecord(c.ev[0], s), "hipEventRecord")) return st;
+  }
+  const int64_t MF = c.batch * c.M, NF = c.batch * c.N;
+  if (MF == 0 || NF == 0) {
+    if (c.ev)
+      for (int e = 1; e < 5; ++e)
+        if (int st = check_hip(hipEventRecord(c.ev[e], s), "hipEventRecord")) return st;
+    return FP64EMU_OK;
+  }
+  if (!c.out || !c.A || !c.B) return fail(FP64EMU_EINVAL, "null operand pointer");
+  if (!c.ws || c.ws_bytes < L.total) return fail(FP64EMU_EWORKSPACE, "workspace too small");
+  const ModTables tab = make_tables(c.primes, c.P);
+
+  char* ws = static_cast<char*>(c.ws);
+  int16_t* sftA = reinterpret_cast<int16_t*>(ws + L.off_sftA);
+  int16_t* sftB = reinterpret_cast<int16_t*>(ws + L.off_sftB);
+  float* lgA = reinterpret_cast<float*>(ws + L.off_lgA);
+  float* lgB = reinterpret_cast<float*>(ws + L.off_lgB);
+  int* bits_eff = reinterpret_cast<int*>(ws + L.off_bits);
+  double* pmax = reinterpret_cast<double*>(ws + L.off_pmax);
+  double* pss = reinterpret_cast<double*>(ws + L.off_pss);
+  int8_t* planesA = reinterpret_cast<int8_t*>(ws + L.off_planesA);
+  int8_t* planesB = reinterpret_cast<int8_t*>(ws + L.off_planesB);
+  int8_t* res8 = reinterpret_cast<int8_t*>(ws + L.off_res8);
+  int32_t* corr = reinterpret_cast<int32_t*>(ws + L.off_corr);
+
+  // 1. sizing
+  if (!c.b_kn) {
+    hipLaunchKernelGGL(size_rows_kernel, dim3((unsigned)(MF + NF)), dim3(kThreads), 0, s, c.A, MF,
+                       c.B, c.K, c.bits, sftA, lgA, sftB, lgB);
+  } else {
+    hipLaunchKernelGGL(size_rows_kernel, dim3((unsigned)MF), dim3(kThreads), 0, s, c.A, MF, c.A,
+                       c.K, c.bits, sftA, lgA, sftB, lgB);
+    int64_t kslab; int nslab;
+    slab_split(NF, c.K, &kslab, &nslab);
+    const unsigned gcx = (unsigned)((NF + kThreads - 1) / kThreads);
+    if (nslab > 0)
+      hipLaunchKernelGGL(size_cols_partial_kernel, dim3(gcx, (unsigned)nslab), dim3(kThreads), 0, s,
+                         c.B, NF, c.K, c.N, kslab, pmax, pss);
+    hipLaunchKernelGGL(size_cols_final_kernel, dim3(gcx), dim3(kThreads), 0, s, pmax, pss, NF,
+                       nslab, c.bits, sftB, lgB);
+  }
+  hipLaunchKernelGGL(pick_width_kernel, dim3(1), dim3(kThreads), 0, s, lgA, MF, lgB, NF,
+                     std::min(tab.log2M, 126.0f), c.bits, sftA, sftB, bits_eff);
+
+  // 2. extraction (covers the padded planes entirely: no memset needed)
+  const int64_t nkt = L.Kp / kTileK;
+  if (nkt > 0) {
+    ExtractArgs ea;
+    ea.A = c.A; ea.B = c.B;
+    ea.M = c.M; ea.N = c.N; ea.K = c.K; ea.batch = c.batch;
+    ea.b_kn = c.b_kn ? 1 : 0;
+    ea.use_corr = c.corr ? 1 : 0;
+    ea.nkt = nkt;
+    ea.planeA = L.planeA_bytes; ea.planeB = L.planeB_bytes;
+    ea.memberA = L.memberA_bytes; ea.memberB = L.memberB_bytes;
+    ea.rgA = L.Mp / 64; ea.rgB = L.Np / 64;
+    ea.wgA = c.batch * ea.rgA * nkt;
+    ea.sftA = sftA; ea.sftB = sftB; ea.bits_eff = bits_eff;
+    ea.planesA = planesA; ea.planesB = planesB;
+    ea.tab = tab;
+    const int64_t wg = ea.wgA + c.batch * ea.rgB * nkt;
+    hipLaunchKernelGGL(extract_kernel, dim3((unsigned)wg), dim3(kThreads), 0, s, ea);
+  }
+  if (c.ev) {
+    if (int st = check_hip(hipEventRecord(c.ev[1], s), "hipEventRecord")) return st;
+  }
+
+  // 3. modular GEMMs
+  {
+    GemmArgs ga;
+    ga.A = planesA; ga.B = planesB; ga.res8 = res8; ga.corr = corr;
+    ga.memberA = L.memberA_bytes; ga.memberB = L.memberB_bytes;
+    ga.planeA = L.planeA_bytes; ga.planeB = L.planeB_bytes;
+    ga.outplane = L.outplane_bytes;
+    ga.nkt = (int)nkt;
+    ga.TM = (int)(L.Mp / kTileR); ga.TN = (int)(L.Np / kTileR);
+    ga.P = c.P; ga.ncorr = L.ncorr; ga.nslots = c.P + L.ncorr; ga.batch = (int)c.batch;
+    for (int t = 0; t < kMaxP; ++t) { ga.p[t] = tab.p[t]; ga.invp[t] = tab.invp[t]; }
+    ga.total = (int64_t)ga.nslots * c.batch * ga.TM * ga.TN;
+    hipLaunchKernelGGL(modgemm_kernel, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+  }
+  if (c.ev) {
+    if (int st = check_hip(hipEventRecord(c.ev[2], s), "hipEventRecord")) return st;
+    if (int st = check_hip(hipEventRecord(c.ev[3], s), "hipEventRecord")) return st;
+  }
+
+  // 4. reconstruction
+  {
+    ReconArgs ra;
+    ra.res8 = res8; ra.corr = corr; ra.out = c.out;
+    ra.sftA = sftA; ra.sftB = sftB; ra.bits_eff = bits_eff;
+    ra.M = c.M; ra.N = c.N; ra.batch = c.batch; ra.outplane = L.outplane_bytes;
+    ra.NB = L.Np / 16;
+    ra.MBv = (c.M + 15) / 16; ra.NBv = (c.N + 15) / 16;
+    ra.nblocks = c.batch * ra.MBv * ra.NBv;
+    ra.ncorr = L.ncorr;
+    ra.tab = tab;
+    const unsigned grid = (unsigned)((ra.nblocks + 3) / 4);
+    if (c.exact)
+      hipLaunchKernelGGL(reconstruct_kernel<true>, dim3(grid), dim3(kThreads), 0, s, ra);
+    else
+      hipLaunchKernelGGL(reconstruct_kernel<false>, dim3(grid), dim3(kThreads), 0, s, ra);
+  }
+  if (int st = check_hip(hipGetLastError(), "kernel launch")) return st;
+  if (c.ev) {
+    if (int st = check_hip(hipEventRecord(c.ev[4], s), "hipEventRecord")) return st;
+  }
+  return FP64EMU_OK;
+}
+
+Call make_call(double* out, const double* A, const double* B, int64_t batch, int64_t M,
+               int64_t N, int64_t K, bool b_kn, const int32_t* primes, int nprimes, int exact,
+               int64_t bits, int use_corr, void* ws, size_t ws_bytes, fp64emu_stream_t stream) {
+  Call c;
+  c.out = out; c.A = A; c.B = B;
+  c.batch = batch; c.M = M; c.N = N; c.K = K;
+  c.b_kn = b_kn;
+  c.primes = primes; c.P = nprimes;
+  c.exact = exact != 0;
+  c.bits = (bits < 0 || bits > 1000) ? -1 : (int)bits;
+  c.corr = use_corr != 0;
+  c.ws = ws; c.ws_bytes = ws_bytes;
+  c.stream = reinterpret_cast<hipStream_t>(stream);
+  c.ev = nullptr;
+  return c;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+
+extern "C" {
+
+int fp64emu_maxp(void) { return kMaxP; }
+
+const char* fp64emu_last_error(void) { return g_err.c_str(); }
+
+size_t fp64emu_workspace_size(int64_t batch, int64_t M, int64_t N, int64_t K, int nprimes,
+                              int use_corr) {
+  if (batch < 0 || M < 0 || N < 0 || K < 0 || nprimes < 1 || nprimes > kMaxP) return 0;
+  fp64emu_layout_t L;
+  make_layout(batch, M, N, K, nprimes, use_corr != 0, &L);
+  return L.total;
+}
+
+int fp64emu_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int nprimes, int use_corr,
+                   fp64emu_layout_t* out) {
+  g_err.clear();
+  if (!out) return fail(FP64EMU_EINVAL, "layout output must not be NULL");
+  if (batch < 0 || M < 0 || N < 0 || K < 0) return fail(FP64EMU_EINVAL, "shapes must be non-negative");
+  if (nprimes < 1 || nprimes > kMaxP) return fail(FP64EMU_EINVAL, "too many primes");
+  make_layout(batch, M, N, K, nprimes, use_corr != 0, out);
+  return FP64EMU_OK;
+}
+
+int fp64emu_mm(double* out, const double* A, const double* B, int64_t M, int64_t N, int64_t K,
+               const int32_t* primes, const int32_t* inv, const int64_t* mu, int nprimes,
+               int exact, int64_t bits, int use_corr, void* workspace, size_t workspace_bytes,
+               fp64emu_stream_t stream) {
+  (void)inv; (void)mu;
+  g_err.clear();
+  return run(make_call(out, A, B, 1, M, N, K, false, primes, nprimes, exact, bits, use_corr,
+                       workspace, workspace_bytes, stream));
+}
+
+int fp64emu_mm_nt(double* out, const double* A, const double* Bt, int64_t M, int64_t N, int64_t K,
+                  const int32_t* primes, const int32_t* inv, const int64_t* mu, int nprimes,
+                  int exact, int64_t bits, int use_corr, void* workspace, size_t workspace_bytes,
+                  fp64emu_stream_t stream) {
+  (void)inv; (void)mu;
+  g_err.clear();
+  return run(make_call(out, A, Bt, 1, M, N, K, true, primes, nprimes, exact, bits, use_corr,
+                       workspace, workspace_bytes, stream));
+}
+
+int fp64emu_bmm(double* out, const double* A, const double* B, int64_t batch, int64_t M, int64_t N,
+                int64_t K, const int32_t* primes, const int32_t* inv, const int64_t* mu,
+                int nprimes, int exact, int64_t bits, int use_corr, void* workspace,
+                size_t workspace_bytes, fp64emu_stream_t stream) {
+  (void)inv; (void)mu;
+  g_err.clear();
+  return run(make_call(out, A, B, batch, M, N, K, false, primes, nprimes, exact, bits, use_corr,
+                       workspace, workspace_bytes, stream));
+}
+
+int fp64emu_bmm_nt(double* out, const double* A, const double* Bt, int64_t batch, int64_t M,
+                   int64_t N, int64_t K, const int32_t* primes, const int32_t* inv,
+                   const int64_t* mu, int nprimes, int exact, int64_t bits, int use_corr,
+                   void* workspace, size_t workspace_bytes, fp64emu_stream_t stream) {
+  (void)inv; (void)mu;
+  g_err.clear();
+  return run(make_call(out, A, Bt, batch, M, N, K, true, primes, nprimes, exact, bits, use_corr,
+                       workspace, workspace_bytes, stream));
+}
+
+int fp64emu_mm_timed(double* out, float* times, const double* A, const double* B, int64_t M,
+                     int64_t N, int64_t K, const int32_t* primes, const int32_t* inv,
+                     const int64_t* mu, int nprimes, int exact, int64_t bits, int use_corr,
+                     void* workspace, size_t workspace_bytes, fp64emu_stream_t stream) {
+  (void)inv; (void)mu;
+  g_err.clear();
+  if (!times) return fail(FP64EMU_EINVAL, "times must not be NULL");
+  Call c = make_call(out, A, B, 1, M, N, K, false, primes, nprimes, exact, bits, use_corr,
+                     workspace, workspace_bytes, stream);
+  hipEvent_t ev[5];
+  int created = 0;
+  int st = FP64EMU_OK;
+  for (; created < 5; ++created) {
+    st = check_hip(hipEventCreate(&ev[created]), "hipEventCreate");
+    if (st) break;
+  }
+  if (!st) {
+    c.ev = ev;
+    st = run(c);
+  }
+  if (!st) st = check_hip(hipEventSynchronize(ev[4]), "hipEventSynchronize");
+  if (!st) {
+    for (int i = 0; i < 4 && !st; ++i)
+      st = check_hip(hipEventElapsedTime(&times[i], ev[i], ev[i + 1]), "hipEventElapsedTime");
+  }
+  for (int i = 0; i < created; ++i) (void)hipEventDestroy(ev[i]);
+  return st;
+}
+
+int fp64emu_ddgemm_nt(double* hi, double* lo, const double* A, const double* B, int64_t M,
+                      int64_t N, int64_t K, fp64emu_stream_t stream) {
+  g_err.clear();
+  if (M < 0 || N < 0 || K < 0) return fail(FP64EMU_EINVAL, "shapes must be non-negative");
+  if (M == 0 || N == 0) return FP64EMU_OK;
+  if (!hi || !lo || !A || !B) return fail(FP64EMU_EINVAL, "null operand pointer");
+  const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
+  hipLaunchKernelGGL(ddgemm_nt_kernel, grid, dim3(kThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), hi, lo, A, B, M, N, K);
+  return check_hip(hipGetLastError(), "ddgemm launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,234 @@
+"""ctypes binding of the C ABI (include/fp64emu.h) plus host-side decoders of
+the workspace map, for stage-level inspection by tests and the bench.
+
+Calls go straight to libfp64emu.so with device pointers from torch tensors
+and the current torch stream; no torch C++ is involved.  Decoders turn the
+tile-blocked operand planes and the blocked output planes back into logical
+[rows, K] / [M, N] arrays (numpy).
+"""
+import ctypes
+import os
+
+import numpy as np
+import torch  # loads torch's HIP runtime before libfp64emu.so binds to it
+
+from . import _ops  # noqa: F401  (fails loudly when the extension is missing)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+CAPI_PATH = os.path.join(_HERE, "libfp64emu.so")
+
+TILE_R, TILE_K, FRAG = 256, 64, 1024
+
+# Every function declared in include/fp64emu.h.
+EXPORTS = ("fp64emu_maxp", "fp64emu_last_error", "fp64emu_workspace_size", "fp64emu_mm",
+           "fp64emu_mm_nt", "fp64emu_bmm", "fp64emu_bmm_nt", "fp64emu_mm_timed",
+           "fp64emu_layout", "fp64emu_ddgemm_nt")
+
+
+class Layout(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_int64), ("M", ctypes.c_int64), ("N", ctypes.c_int64),
+                ("K", ctypes.c_int64), ("nprimes", ctypes.c_int), ("use_corr", ctypes.c_int),
+                ("ncorr", ctypes.c_int), ("nslab", ctypes.c_int), ("Mp", ctypes.c_int64),
+                ("Np", ctypes.c_int64), ("Kp", ctypes.c_int64), ("planeA_bytes", ctypes.c_int64),
+                ("planeB_bytes", ctypes.c_int64), ("memberA_bytes", ctypes.c_int64),
+                ("memberB_bytes", ctypes.c_int64), ("outplane_bytes", ctypes.c_int64)] + [
+                   (n, ctypes.c_size_t) for n in (
+                       "off_sftA", "off_sftB", "off_lgA", "off_lgB", "off_bits", "off_pmax",
+                       "off_pss", "off_planesA", "off_planesB", "off_res8", "off_corr", "total")]
+
+    def as_dict(self):
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+_LIB = None
+
+
+def lib():
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    L = ctypes.CDLL(CAPI_PATH)
+    i64, i32, vp, sz = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
+    L.fp64emu_maxp.restype = i32
+    L.fp64emu_last_error.restype = ctypes.c_char_p
+    L.fp64emu_workspace_size.argtypes = [i64, i64, i64, i64, i32, i32]
+    L.fp64emu_workspace_size.restype = sz
+    mm_args = [vp, vp, vp, i64, i64, i64, vp, vp, vp, i32, i32, i64, i32, vp, sz, vp]
+    for name in ("fp64emu_mm", "fp64emu_mm_nt"):
+        getattr(L, name).argtypes = mm_args
+        getattr(L, name).restype = i32
+    bmm_args = [vp, vp, vp, i64, i64, i64, i64, vp, vp, vp, i32, i32, i64, i32, vp, sz, vp]
+    for name in ("fp64emu_bmm", "fp64emu_bmm_nt"):
+        getattr(L, name).argtypes = bmm_args
+        getattr(L, name).restype = i32
+    L.fp64emu_mm_timed.argtypes = [vp, vp, vp, vp, i64, i64, i64, vp, vp, vp, i32, i32, i64, i32,
+                                   vp, sz, vp]
+    L.fp64emu_mm_timed.restype = i32
+    L.fp64emu_layout.argtypes = [i64, i64, i64, i64, i32, i32, ctypes.POINTER(Layout)]
+    L.fp64emu_layout.restype = i32
+    L.fp64emu_ddgemm_nt.argtypes = [vp, vp, vp, vp, i64, i64, i64, vp]
+    L.fp64emu_ddgemm_nt.restype = i32
+    _LIB = L
+    return L
+
+
+class CapiError(RuntimeError):
+    pass
+
+
+def _check(st):
+    if st != 0:
+        raise CapiError(lib().fp64emu_last_error().decode())
+
+
+def layout(batch, M, N, K, nprimes, use_corr):
+    out = Layout()
+    _check(lib().fp64emu_layout(batch, M, N, K, nprimes, int(bool(use_corr)), ctypes.byref(out)))
+    return out
+
+
+def workspace_size(batch, M, N, K, nprimes, use_corr):
+    return lib().fp64emu_workspace_size(batch, M, N, K, nprimes, int(bool(use_corr)))
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def run(kind, A, B, primes, exact=True, bits=53, use_corr=True, out=None, ws=None):
+    """Call fp64emu_{mm,mm_nt,bmm,bmm_nt} on device tensors.  Returns
+    (out, ws, layout); `ws` holds the call's intermediates afterwards."""
+    primes = np.ascontiguousarray(np.asarray(primes, dtype=np.int32))
+    P = int(primes.size)
+    batched = kind in ("bmm", "bmm_nt")
+    if batched:
+        batch, M, K = A.shape
+        N = B.shape[2] if kind == "bmm_nt" else B.shape[1]
+    else:
+        batch = 1
+        M, K = A.shape
+        N = B.shape[1] if kind == "mm_nt" else B.shape[0]
+    lay = layout(batch, M, N, K, P, use_corr)
+    if ws is None:
+        ws = torch.empty(max(int(lay.total), 1), dtype=torch.uint8, device=A.device)
+    if out is None:
+        shape = (batch, M, N) if batched else (M, N)
+        out = torch.empty(shape, dtype=torch.float64, device=A.device)
+    pp = primes.ctypes.data_as(ctypes.c_void_p)
+    fn = getattr(lib(), "fp64emu_" + kind)
+    common = (pp, None, None, P, int(bool(exact)), int(bits), int(bool(use_corr)),
+              ws.data_ptr(), ws.numel(), _stream())
+    if batched:
+        st = fn(out.data_ptr(), A.data_ptr(), B.data_ptr(), batch, M, N, K, *common)
+    else:
+        st = fn(out.data_ptr(), A.data_ptr(), B.data_ptr(), M, N, K, *common)
+    _check(st)
+    return out, ws, lay
+
+
+def mm_timed(A, B, primes, exact=True, bits=53, use_corr=True):
+    primes = np.ascontiguousarray(np.asarray(primes, dtype=np.int32))
+    M, K = A.shape
+    N = B.shape[0]
+    lay = layout(1, M, N, K, primes.size, use_corr)
+    ws = torch.empty(max(int(lay.total), 1), dtype=torch.uint8, device=A.device)
+    out = torch.empty((M, N), dtype=torch.float64, device=A.device)
+    times = (ctypes.c_float * 4)()
+    _check(lib().fp64emu_mm_timed(out.data_ptr(), times, A.data_ptr(), B.data_ptr(), M, N, K,
+                                  primes.ctypes.data_as(ctypes.c_void_p), None, None,
+                                  primes.size, int(bool(exact)), int(bits),
+                                  int(bool(use_corr)), ws.data_ptr(), ws.numel(), _stream()))
+    return out, list(times)
+
+
+def ddgemm_nt(A, B):
+    """Double-double C = A @ B^T on the device (A [M,K], B [N,K])."""
+    M, K = A.shape
+    N = B.shape[0]
+    hi = torch.empty((M, N), dtype=torch.float64, device=A.device)
+    lo = torch.empty_like(hi)
+    _check(lib().fp64emu_ddgemm_nt(hi.data_ptr(), lo.data_ptr(), A.data_ptr(), B.data_ptr(),
+                                   M, N, K, _stream()))
+    return hi, lo
+
+
+# ---- workspace decoders (host, numpy) --------------------------------------
+
+def _ws_bytes(ws):
+    if isinstance(ws, torch.Tensor):
+        return ws.cpu().numpy()
+    return np.asarray(ws, dtype=np.uint8)
+
+
+def sizing(ws, lay):
+    """(sftA [batch*M], sftB [batch*N], lgA, lgB, bits_eff) after the call."""
+    w = _ws_bytes(ws)
+    MF, NF = lay.batch * lay.M, lay.batch * lay.N
+    sftA = w[lay.off_sftA:lay.off_sftA + 2 * MF].view(np.int16).copy()
+    sftB = w[lay.off_sftB:lay.off_sftB + 2 * NF].view(np.int16).copy()
+    lgA = w[lay.off_lgA:lay.off_lgA + 4 * MF].view(np.float32).copy()
+    lgB = w[lay.off_lgB:lay.off_lgB + 4 * NF].view(np.float32).copy()
+    be = int(w[lay.off_bits:lay.off_bits + 4].view(np.int32)[0])
+    return sftA, sftB, lgA, lgB, be
+
+
+def _plane_to_logical(raw, rows_p, depth_p):
+    """One tile-blocked plane (bytes) -> int8 [rows_p, depth_p].  Inside a
+    256 x 64 tile: 16 fragments of 16 rows; in a fragment, lane
+    l = 16*(k//16) + row%16 holds k%16 at byte 16*l + k%16."""
+    nrt, nkt = rows_p // TILE_R, depth_p // TILE_K
+    a = raw.view(np.int8).reshape(nrt, nkt, 16, 4, 16, 16)   # rt kt fr kc r16 kb
+    return a.transpose(0, 2, 4, 1, 3, 5).reshape(rows_p, depth_p)
+
+
+def planes(ws, lay, operand):
+    """Operand planes of the call: (res [batch, P, rows, K],
+    hi [batch, rows, K], q [batch, rows, K]) with padding stripped, plus the
+    padded arrays for padding checks: (res_p, corr_p)."""
+    w = _ws_bytes(ws)
+    isA = operand == "A"
+    rows, rows_p = (lay.M, lay.Mp) if isA else (lay.N, lay.Np)
+    off = lay.off_planesA if isA else lay.off_planesB
+    member = lay.memberA_bytes if isA else lay.memberB_bytes
+    plane = lay.planeA_bytes if isA else lay.planeB_bytes
+    P, Kp, K = lay.nprimes, lay.Kp, lay.K
+    res_p = np.zeros((lay.batch, P, rows_p, Kp), dtype=np.int8)
+    corr_p = np.zeros((lay.batch, rows_p, 2 * Kp), dtype=np.int8) if lay.use_corr else None
+    for b in range(lay.batch):
+        base = off + b * member
+        for t in range(P):
+            raw = w[base + t * plane: base + (t + 1) * plane]
+            res_p[b, t] = _plane_to_logical(raw, rows_p, Kp)
+        if lay.use_corr and Kp > 0:
+            raw = w[base + P * plane: base + (P + 2) * plane]
+            corr_p[b] = _plane_to_logical(raw, rows_p, 2 * Kp)
+    res = res_p[:, :, :rows, :K]
+    if lay.use_corr:
+        first, second = corr_p[:, :rows, :K], corr_p[:, :rows, Kp:Kp + K]
+        hi, q = (first, second) if isA else (second, first)
+    else:
+        hi = q = None
+    return res, hi, q, res_p, corr_p
+
+
+def _blocks_to_logical(arr, Mp, Np):
+    """Blocked output plane -> [Mp, Np].  16x16 blocks row-block major; in a
+    block, element (r, c) sits at 64*(r//4) + 4*c + r%4."""
+    a = arr.reshape(Mp // 16, Np // 16, 4, 16, 4)             # mb nb rq c rr
+    return a.transpose(0, 2, 4, 1, 3).reshape(Mp, Np)
+
+
+def outputs(ws, lay):
+    """(res8 [batch, P, M, N] int8, corr [batch, ncorr, M, N] int32)."""
+    w = _ws_bytes(ws)
+    P, Mp, Np, ob = lay.nprimes, lay.Mp, lay.Np, lay.outplane_bytes
+    res = np.zeros((lay.batch, P, lay.M, lay.N), dtype=np.int8)
+    corr = np.zeros((lay.batch, lay.ncorr, lay.M, lay.N), dtype=np.int32)
+    for b in range(lay.batch):
+        for t in range(P):
+            s = lay.off_res8 + (b * P + t) * ob
+            res[b, t] = _blocks_to_logical(w[s:s + ob].view(np.int8), Mp, Np)[:lay.M, :lay.N]
+        for c in range(lay.ncorr):
+            s = lay.off_corr + 4 * (b * lay.ncorr + c) * ob
+            corr[b, c] = _blocks_to_logical(w[s:s + 4 * ob].view(np.int32), Mp, Np)[:lay.M, :lay.N]
+    return res, corr

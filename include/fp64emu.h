@@ -1,0 +1,133 @@
+/*
+ * fp64emu.h -- C ABI of the MI355X-native RARE emulated-FP64 GEMM.
+ *
+ * C = A @ B in float64 is recovered from INT8 products modulo up to 20
+ * pairwise-coprime moduli (one CDNA4 INT8-MFMA GEMM each), a first-order
+ * quantization correction (hi7 x q7 cross GEMMs) and balanced-Garner
+ * reconstruction.  Every entry point enqueues asynchronously on `stream`
+ * and allocates nothing: the caller passes a device workspace of at least
+ * fp64emu_workspace_size() bytes (the torch binding takes it from the
+ * caching allocator, which keeps the call graph-capturable).  All pointers
+ * are device pointers unless the parameter says "host".
+ *
+ * Return value: 0 on success, nonzero on error; fp64emu_last_error() then
+ * holds the message (thread-local).  The messages of argument errors are
+ * the reference's TORCH_CHECK texts.
+ *
+ * Reference interface each entry point replaces (paths relative to the
+ * upstream fp64-emu checkout):
+ *   torch-ext/torch_binding.cpp:7-12   op schemas
+ *   torch-ext/torch_binding.h:5-21     C++ signatures
+ *   fp64_emu_cuda/fp64_emu.cu:956      fp64_emu_maxp
+ *   fp64_emu_cuda/fp64_emu.cu:1583     fp64_emu_mm
+ *   fp64_emu_cuda/fp64_emu.cu:1613     fp64_emu_mm_nt
+ *   fp64_emu_cuda/fp64_emu.cu:1637     fp64_emu_bmm
+ *   fp64_emu_cuda/fp64_emu.cu:1665     fp64_emu_bmm_nt
+ *   fp64_emu_cuda/fp64_emu.cu:1688     fp64_emu_mm_timed
+ * The reference's `Tensor primes_cpu, Tensor inv_cpu, Tensor mu_cpu` become
+ * host pointers plus `nprimes`; like the reference (fp64_emu.cu:1137-1140)
+ * the library derives its own tables from `primes` and ignores `inv`/`mu`,
+ * which may be NULL.
+ */
+#ifndef FP64EMU_H
+#define FP64EMU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t, kept opaque so this header needs no HIP include. */
+typedef struct ihipStream_t* fp64emu_stream_t;
+
+#define FP64EMU_MAXP 20
+
+enum {
+  FP64EMU_OK = 0,
+  FP64EMU_EINVAL = 1,     /* argument check failed (reference TORCH_CHECK) */
+  FP64EMU_EWORKSPACE = 2, /* workspace missing or too small */
+  FP64EMU_EHIP = 3        /* HIP runtime error (launch, event) */
+};
+
+/* fp64_emu_cuda/fp64_emu.cu:956 -- the largest modulus count (20). */
+int fp64emu_maxp(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* fp64emu_last_error(void);
+
+/* Device workspace bytes needed by one call with these shapes (per batch
+ * member M, N, K).  Replaces the per-call torch::empty/zeros scratch of
+ * run_crt (fp64_emu_cuda/fp64_emu.cu:1148-1151, 1255-1256, 1344-1345). */
+size_t fp64emu_workspace_size(int64_t batch, int64_t M, int64_t N, int64_t K,
+                              int nprimes, int use_corr);
+
+/* out[M,N] = A[M,K] @ B[N,K]^T.   fp64_emu_cuda/fp64_emu.cu:1583-1608 */
+int fp64emu_mm(double* out, const double* A, const double* B, int64_t M, int64_t N, int64_t K,
+               const int32_t* primes /* host */, const int32_t* inv /* host, unused */,
+               const int64_t* mu /* host, unused */, int nprimes, int exact, int64_t bits,
+               int use_corr, void* workspace, size_t workspace_bytes, fp64emu_stream_t stream);
+
+/* out[M,N] = A[M,K] @ Bt[K,N], Bt consumed in its [K,N] layout (no
+ * transpose copy).   fp64_emu_cuda/fp64_emu.cu:1613-1632 */
+int fp64emu_mm_nt(double* out, const double* A, const double* Bt, int64_t M, int64_t N, int64_t K,
+                  const int32_t* primes, const int32_t* inv, const int64_t* mu, int nprimes,
+                  int exact, int64_t bits, int use_corr, void* workspace, size_t workspace_bytes,
+                  fp64emu_stream_t stream);
+
+/* out[b,M,N] = A[b,M,K] @ B[b,N,K]^T.   fp64_emu_cuda/fp64_emu.cu:1637-1662 */
+int fp64emu_bmm(double* out, const double* A, const double* B, int64_t batch, int64_t M, int64_t N,
+                int64_t K, const int32_t* primes, const int32_t* inv, const int64_t* mu,
+                int nprimes, int exact, int64_t bits, int use_corr, void* workspace,
+                size_t workspace_bytes, fp64emu_stream_t stream);
+
+/* out[b,M,N] = A[b,M,K] @ Bt[b,K,N].   fp64_emu_cuda/fp64_emu.cu:1665-1686 */
+int fp64emu_bmm_nt(double* out, const double* A, const double* Bt, int64_t batch, int64_t M,
+                   int64_t N, int64_t K, const int32_t* primes, const int32_t* inv,
+                   const int64_t* mu, int nprimes, int exact, int64_t bits, int use_corr,
+                   void* workspace, size_t workspace_bytes, fp64emu_stream_t stream);
+
+/* fp64emu_mm plus phase times in ms, written to the host array
+ * times[4] = [sizing+extract, gemms, 0-marker, reconstruct]; synchronizes
+ * on the last phase event.   fp64_emu_cuda/fp64_emu.cu:1688-1704 */
+int fp64emu_mm_timed(double* out, float* times /* host, 4 floats */, const double* A,
+                     const double* B, int64_t M, int64_t N, int64_t K, const int32_t* primes,
+                     const int32_t* inv, const int64_t* mu, int nprimes, int exact, int64_t bits,
+                     int use_corr, void* workspace, size_t workspace_bytes,
+                     fp64emu_stream_t stream);
+
+/* ---- Workspace map (inspection of intermediates; no reference
+ * counterpart: the reference's scratch is private torch tensors).  After a
+ * call, the workspace holds that call's sizing outputs, operand planes,
+ * residue planes and correction planes at these byte offsets. ---- */
+typedef struct {
+  int64_t batch, M, N, K;   /* per batch member */
+  int nprimes, use_corr;
+  int ncorr;                /* int32 correction planes per member: 1 (fused, K <= 65536) or 2 */
+  int nslab;                /* column-sizing slabs for a [K,N] operand */
+  int64_t Mp, Np, Kp;       /* padded to the 256-row tile and the 64-deep k tile */
+  int64_t planeA_bytes;     /* one residue plane of A for one member: Mp*Kp */
+  int64_t planeB_bytes;     /* Np*Kp; the correction plane is twice as deep (2*Kp) */
+  int64_t memberA_bytes;    /* all planes of one member: (nprimes + 2*use_corr) * Mp*Kp */
+  int64_t memberB_bytes;
+  int64_t outplane_bytes;   /* one int8 residue output plane: Mp*Np */
+  size_t off_sftA, off_sftB, off_lgA, off_lgB, off_bits, off_pmax, off_pss;
+  size_t off_planesA, off_planesB, off_res8, off_corr, total;
+} fp64emu_layout_t;
+
+int fp64emu_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int nprimes, int use_corr,
+                   fp64emu_layout_t* out /* host */);
+
+/* ---- Measurement helper (not on the product path): double-double GEMM
+ * C = A @ B^T (A [M,K], B [N,K], row-major), hi/lo outputs [M,N].  The GPU
+ * form of the reference's correct-bits oracle bench/accuracy.py:21-50
+ * (dd_matmul_nt), accumulating each dot product in ~106-bit arithmetic. */
+int fp64emu_ddgemm_nt(double* hi, double* lo, const double* A, const double* B, int64_t M,
+                      int64_t N, int64_t K, fp64emu_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FP64EMU_H */

@@ -1,0 +1,115 @@
+"""Stage-by-stage parity of one HIP call against the CPU oracle.
+
+`check_call` runs one C-ABI call, then compares, in order:
+  sizing   shifts (exact), log2-norms (float equality up to 1 ulp on a tiny
+           fraction, from log2 implementations), bits_eff (exact);
+  planes   residue / hi7 / q7 planes, bit-exact against the oracle's
+           extraction at the GPU's shifts and width; padding all zero;
+  outputs  int8 residue planes and int32 correction sums of the GEMMs,
+           bit-exact against the oracle's modular GEMM of those planes;
+  result   the float64 output, bit-exact against the oracle's
+           reconstruction of the GPU's residues, and against the oracle's
+           whole pipeline.
+"""
+import numpy as np
+import torch
+
+import oracle as O
+from fp64_emu import capi
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(np.asarray(a, dtype=np.float64))
+    b = np.ascontiguousarray(np.asarray(b, dtype=np.float64))
+    return a.shape == b.shape and np.array_equal(a.view(np.uint64), b.view(np.uint64))
+
+
+def oracle_sizing(A, B, b_kn, primes, bits):
+    """Oracle sizing of the call's operands (before the width pick)."""
+    A = np.asarray(A)
+    if A.ndim == 2:
+        A = A[None]
+    B = np.asarray(B)
+    if B.ndim == 2:
+        B = B[None]
+    sA, lA = O.size_rows(A.reshape(-1, A.shape[-1]), bits)
+    if b_kn:
+        sB, lB = O.size_cols(B, bits)
+    else:
+        sB, lB = O.size_rows(B.reshape(-1, B.shape[-1]), bits)
+    _, _, _, log2M = O.tables(primes)
+    be, sA2, sB2 = O.pick_bits(lA, lB, min(log2M, 126.0), bits, sA, sB)
+    return be, sA2, sB2, lA, lB
+
+
+def check_call(kind, A, B, primes, exact=True, bits=53, use_corr=True, full_oracle=True):
+    """A, B: device float64 tensors in the layout `kind` expects."""
+    b_kn = kind in ("mm_nt", "bmm_nt")
+    out, ws, lay = capi.run(kind, A, B, primes, exact=exact, bits=bits, use_corr=use_corr)
+    torch.cuda.synchronize()
+    Ah, Bh = A.cpu().numpy(), B.cpu().numpy()
+    primes = np.asarray(primes, dtype=np.int32)
+    P = primes.size
+    wsh = ws.cpu().numpy()
+
+    # sizing
+    gsA, gsB, glA, glB, gbe = capi.sizing(wsh, lay)
+    obe, osA, osB, olA, olB = oracle_sizing(Ah, Bh, b_kn, primes, bits)
+    for g, o in ((glA, olA), (glB, olB)):
+        neq = g != o
+        if neq.any():
+            # log2 of the same fp64 sum may differ by an ulp between libm's;
+            # the float then differs by at most one ulp, rarely.
+            gi, oi = g[neq].view(np.int32).astype(np.int64), o[neq].view(np.int32).astype(np.int64)
+            assert np.all(np.abs(gi - oi) <= 1), "log2-norms differ by more than 1 ulp"
+            assert neq.mean() < 1e-3
+    assert gbe == obe, f"bits_eff GPU {gbe} oracle {obe}"
+    assert np.array_equal(gsA, osA) and np.array_equal(gsB, osB), "shifts differ"
+
+    # planes (at the GPU's sizing)
+    batch = lay.batch
+    A3 = Ah if Ah.ndim == 3 else Ah[None]
+    B3 = Bh if Bh.ndim == 3 else Bh[None]
+    oresA, ohA, oqA = O.extract_operand(A3, 0, gsA, gbe, primes, use_corr)
+    oresB, ohB, oqB = O.extract_operand(B3, 1 if b_kn else 0, gsB, gbe, primes, use_corr)
+    gresA, ghA, gqA, gresA_p, gcorrA_p = capi.planes(wsh, lay, "A")
+    gresB, ghB, gqB, gresB_p, gcorrB_p = capi.planes(wsh, lay, "B")
+    assert np.array_equal(gresA, oresA), "A residue planes differ"
+    assert np.array_equal(gresB, oresB), "B residue planes differ"
+    M, N, K = lay.M, lay.N, lay.K
+    pad = np.ones(gresA_p.shape, bool)
+    pad[:, :, :M, :K] = False
+    assert not gresA_p[pad].any(), "A padding not zero"
+    pad = np.ones(gresB_p.shape, bool)
+    pad[:, :, :N, :K] = False
+    assert not gresB_p[pad].any(), "B padding not zero"
+    if use_corr:
+        assert np.array_equal(ghA, ohA) and np.array_equal(gqA, oqA), "A hi7/q7 differ"
+        assert np.array_equal(ghB, ohB) and np.array_equal(gqB, oqB), "B hi7/q7 differ"
+
+    # GEMM outputs
+    gres8, gcorr = capi.outputs(wsh, lay)
+    for b in range(batch):
+        for t in range(P):
+            o8 = O.modgemm(oresA[b, t], oresB[b, t], int(primes[t]))
+            assert np.array_equal(gres8[b, t], o8), f"residue GEMM {t} (member {b}) differs"
+        if use_corr:
+            oc = (O.modgemm(ohA[b], oqB[b], 0).astype(np.int64)
+                  + O.modgemm(oqA[b], ohB[b], 0).astype(np.int64))
+            gc = gcorr[b].astype(np.int64).sum(axis=0)
+            assert np.array_equal(gc, oc), f"correction GEMMs (member {b}) differ"
+
+    # result
+    outh = out.cpu().numpy()
+    out3 = outh if outh.ndim == 3 else outh[None]
+    for b in range(batch):
+        c1 = gcorr[b].astype(np.int64).sum(axis=0).astype(np.int32) if use_corr else None
+        rec = O.reconstruct(gres8[b], c1, None, primes, gbe, gsA[b * M:(b + 1) * M],
+                            gsB[b * N:(b + 1) * N], exact)
+        assert bits_equal(out3[b], rec), f"reconstruction (member {b}) differs"
+    if full_oracle:
+        oout, info = O.mm(Ah, Bh, 1 if b_kn else 0, primes, exact=exact, bits=bits,
+                          use_corr=use_corr)
+        assert info["bits_eff"] == gbe
+        assert bits_equal(outh, oout), "whole pipeline differs from the oracle"
+    return out, ws, lay

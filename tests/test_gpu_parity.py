@@ -1,0 +1,68 @@
+"""GPU parity of every stage of the HIP path against the CPU oracle, through
+the C ABI, on seeded CPU-generated inputs (configs c1, odd and ragged shapes,
+batched layouts, reduced and inexact operating points)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from parity_util import check_call
+
+pytestmark = pytest.mark.gpu
+
+
+def _randn(shape, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, dtype=torch.float64, generator=g).to(dev)
+
+
+CASES = [
+    # kind, batch, M, N, K, nprimes, corr
+    ("mm_nt", 1, 128, 128, 4096, 14, True),     # c1 plumbing config
+    ("mm_nt", 1, 17, 29, 23, 14, True),
+    ("mm", 1, 129, 127, 4095, 14, True),
+    ("mm", 1, 300, 520, 200, 15, True),
+    ("mm_nt", 1, 257, 255, 129, 13, False),     # reduced operating point
+    ("bmm_nt", 3, 100, 77, 333, 14, True),
+    ("bmm", 5, 96, 64, 256, 14, True),
+    ("mm", 1, 64, 48, 64, 20, True),
+]
+
+
+@pytest.mark.parametrize("kind,batch,M,N,K,P,corr", CASES)
+def test_stage_parity(dev, kind, batch, M, N, K, P, corr):
+    print(f"case {kind} b={batch} {M}x{N}x{K} P={P} corr={corr}", flush=True)
+    seed = 1000 * batch + M + 7 * N + 13 * K
+    if kind in ("bmm", "bmm_nt"):
+        A = _randn((batch, M, K), seed, dev)
+        B = _randn((batch, K, N) if kind == "bmm_nt" else (batch, N, K), seed + 1, dev)
+    else:
+        A = _randn((M, K), seed, dev)
+        B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
+    check_call(kind, A, B, O.PRIMES[:P], use_corr=corr)
+
+
+def test_inexact_parity(dev):
+    print("case inexact mm_nt 96x80x1000", flush=True)
+    A = _randn((96, 1000), 5, dev)
+    B = _randn((1000, 80), 6, dev)
+    check_call("mm_nt", A, B, O.PRIMES[:14], exact=False)
+
+
+def test_narrow_bits_parity(dev):
+    print("case bits=40 mm 64x64x512", flush=True)
+    A = _randn((64, 512), 7, dev)
+    B = _randn((64, 512), 8, dev)
+    check_call("mm", A, B, O.PRIMES[:O.plan(512, 40)], bits=40)
+
+
+def test_wide_range_parity(dev):
+    """c3a-style entries sign * U[1,2) * 2^e, e in [-20, 20]."""
+    print("case wide-range mm_nt 200x150x700", flush=True)
+    g = torch.Generator().manual_seed(31)
+    def wide(shape):
+        s = torch.randint(0, 2, shape, generator=g) * 2 - 1
+        m = 1 + torch.rand(shape, generator=g, dtype=torch.float64)
+        e = torch.randint(-20, 21, shape, generator=g)
+        return (s * m * torch.pow(2.0, e.double())).to(dev)
+    check_call("mm_nt", wide((200, 700)), wide((700, 150)), O.PRIMES[:14])
