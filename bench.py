@@ -1,0 +1,199 @@
+"""Headline benchmark: effective FP64 TFLOPS of emulated mm_nt at n=8192 with
+the default plan, on one MI355X.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--n 8192] [--no-accuracy]
+                [--no-cpu]
+
+One step = one fp64_emu.mm_nt(A, Bt) call on resident 8192x8192 float64
+operands (iid N(0,1) from CPU seeds 2000/2001, configs[1]).  W untimed
+warm-up calls, then exactly K calls between two device synchronisations;
+value = 2 n^3 / (mean ms per call).  Prints one JSON line.  Besides the
+contract fields it reports: the per-phase ms of mm_timed, native rocBLAS
+DGEMM (torch.matmul float64 on the device) throughput, correct bits of both
+against a device double-double GEMM, the plan-adjusted INT8 roofline
+fraction, the `roofline` object for the dominant kernel (the modular GEMM,
+duration from HIP events bracketing its launch on its stream) and the CPU
+baseline (the oracle port on a bounded sample of the same workload).
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "fp64-emu_amd"))
+
+INT8_PEAK_TOPS = 5000.0    # MI355X dense INT8 MFMA, 5.0 POP/s
+HBM_PEAK_GBS = 8000.0
+METRIC = "effective FP64 TFLOPS, mm_nt n=8192 default plan; correct bits vs double-double"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--n", type=int, default=8192)
+    ap.add_argument("--no-accuracy", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build runs on one GPU only (the emulated GEMM has no "
+              "multi-GPU path); use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import fp64_emu
+    from fp64_emu import capi
+
+    dev = torch.device("cuda:0")
+    n = args.n
+    M = N = K = n
+    P, corr = fp64_emu.plan_config(K)
+    G = P + (2 if corr else 0)
+    flop = 2.0 * M * N * K
+
+    g = torch.Generator().manual_seed(2000)
+    A = torch.randn(M, K, dtype=torch.float64, generator=g).to(dev)
+    g = torch.Generator().manual_seed(2001)
+    Bt = torch.randn(K, N, dtype=torch.float64, generator=g).to(dev)
+    torch.cuda.synchronize()
+    log(f"inputs resident: {n}^3, plan P={P} corr={corr} G={G}")
+
+    for _ in range(args.warmup):
+        C = fp64_emu.mm_nt(A, Bt)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        C = fp64_emu.mm_nt(A, Bt)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1e3 / max(args.steps, 1)
+    value = flop / (ms * 1e-3) / 1e12
+    log(f"timed {args.steps} steps: {ms:.3f} ms/step, {value:.1f} TFLOP/s")
+
+    # Phases and the modular GEMM kernel's duration: mm_timed's events e1/e2
+    # bracket exactly the one modgemm launch, on its stream.
+    B = Bt.t().contiguous()
+    phases = []
+    for _ in range(max(3, args.steps)):
+        _, ph = fp64_emu.mm_timed(A, B)
+        phases.append(ph)
+    avg = [sum(p[i] for p in phases) / len(phases) for i in range(4)]
+    gemm_ms = avg[1]
+    gemm_tops = 2.0 * M * N * K * G / (gemm_ms * 1e-3) / 1e12
+    del B
+    log(f"phases ms (avg of {len(phases)}): {['%.3f' % x for x in avg]}")
+
+    # Native DGEMM comparator (rocBLAS through torch.matmul float64).
+    for _ in range(2):
+        Cn = A @ Bt
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    nat_steps = max(3, min(args.steps, 10))
+    for _ in range(nat_steps):
+        Cn = A @ Bt
+    torch.cuda.synchronize()
+    nat_ms = (time.perf_counter() - t0) * 1e3 / nat_steps
+    nat_tf = flop / (nat_ms * 1e-3) / 1e12
+    log(f"native DGEMM: {nat_ms:.3f} ms, {nat_tf:.1f} TFLOP/s")
+
+    acc = {}
+    if not args.no_accuracy:
+        hi, lo = capi.ddgemm_nt(A, Bt.t().contiguous())
+        torch.cuda.synchronize()
+        scale = hi.abs().max().item()
+
+        def bits(X):
+            err = ((X - hi) - lo).abs().max().item()
+            return 53.0 if err == 0 else -math.log2(err / scale)
+
+        acc = {"correct_bits_emu": round(bits(C), 2), "correct_bits_native": round(bits(Cn), 2)}
+        del hi, lo
+        log(f"correct bits: emu {acc['correct_bits_emu']}, native {acc['correct_bits_native']}")
+    del Cn
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(A, Bt, P, corr)
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "modgemm_c2_traffic.json")
+    if n == 8192 and os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    rec = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": f"mm_nt M=N=K={n}, A/Bt iid N(0,1) (CPU seeds 2000/2001), "
+                               f"default plan_config({K}) = ({P}, corr={corr})",
+                   "M": M, "N": N, "K": K, "nprimes": P, "corr": corr, "gemms": G,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "modgemm_kernel",
+                     "achieved": round(gemm_tops, 1), "peak": INT8_PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
+                     "traffic": traffic,
+                     "work": "2*M*N*K*G INT8 ops per launch"},
+        "plan_roofline_frac": round(value / (INT8_PEAK_TOPS / G), 4),
+        "phases_ms": [round(x, 4) for x in avg],
+        "native_dgemm_tflops": round(nat_tf, 2),
+        "native_dgemm_ms": round(nat_ms, 3),
+        "speedup_vs_native": round(value / nat_tf, 3),
+        **acc,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+def cpu_baseline(A, Bt, P, corr):
+    """The oracle port (the reference pipeline restated in C) on the host's
+    cores, on a bounded sample of the workload: the first 1024 rows of A and
+    columns of Bt at the full depth K, same plan.  Effective FP64 TFLOPS of
+    that sample (2 * 1024 * 1024 * K / t)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    try:
+        import psutil
+        cores = len(psutil.Process().cpu_affinity())
+    except Exception:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    m = 1024
+    a = A[:m].cpu().numpy()
+    bt = Bt[:, :m].contiguous().cpu().numpy()
+    K = a.shape[1]
+    t0 = time.perf_counter()
+    O.mm(a, bt, 1, O.PRIMES[:P], use_corr=corr, nthreads=cores)
+    t = time.perf_counter() - t0
+    val = 2.0 * m * m * K / t / 1e12
+    log(f"cpu baseline (oracle port, {cores} threads): {t:.2f} s, {val:.4f} TFLOP/s")
+    return {"value": round(val, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"mm_nt {m}x{m}x{K} (rows/cols 0..{m - 1} of the workload, full depth), "
+                      f"same plan, oracle/fp64emu_oracle.c with OpenMP",
+            "seconds": round(t, 3)}
+
+
+if __name__ == "__main__":
+    main()

@@ -308,10 +308,12 @@ pick_width_kernel(const float* __restrict__ lgA, int64_t m, const float* __restr
 // the reference's -128.
 //
 // Plane layout (per batch member, per plane): 256-row x 64-k tiles, row tile
-// major, k tile minor; inside a tile, 16 fragments of 16 rows, each 1 KiB in
-// MFMA lane order: lane l = 16 * (k / 16) + (row % 16) holds k % 16 in its
-// 16 bytes.  The correction plane is one 2*Kp-deep plane: A = [hi7 | q7],
-// B = [q7 | hi7], so one GEMM accumulates hi7_A q7_B^T + q7_A hi7_B^T.
+// major, k tile minor; a tile holds 16 fragments of 32 rows x 32 k, fragment
+// f = 2 * (row % 256 / 32) + (k % 64 / 32), each 1 KiB in the operand order of
+// v_mfma_i32_32x32x32_i8: lane l = 32 * (k % 32 / 16) + (row % 32) holds
+// k % 16 at byte 16 * l + k % 16.  The correction plane is one 2*Kp-deep
+// plane: A = [hi7 | q7], B = [q7 | hi7], so one GEMM accumulates
+// hi7_A q7_B^T + q7_A hi7_B^T.
 
 __device__ __forceinline__ uint64_t rne_shift_right(uint64_t mag, int s) {
   if (s <= 0) return (s > -64) ? (mag << (-s)) : 0ull;
@@ -366,9 +368,11 @@ extract_kernel(ExtractArgs a) {
   }
   const int64_t R = isA ? a.M : a.N;
   const int64_t K = a.K;
-  const int64_t rblk = rg * 4 + wave;                // 16-row fragment index
-  const int64_t r = rblk * 16 + (lane & 15);         // plane row (A row or B column)
-  const int64_t k0 = kt * kTileK + (lane >> 4) * 16; // first of this lane's 16 k
+  // Wave w covers rows 64 rg + 32 (w >> 1) .. +32 and k half (w & 1) of the
+  // k tile: one 32x32 fragment.
+  const int64_t rblk = rg * 2 + (wave >> 1);                     // 32-row block
+  const int64_t r = rblk * 32 + (lane & 31);                     // plane row (A row or B column)
+  const int64_t k0 = kt * kTileK + (wave & 1) * 32 + (lane >> 5) * 16;  // first of 16 k
   const bool rowok = r < R;
 
   // Shift: per row of A / of B [N,K]; per column of B [K,N] -- one per lane.
@@ -427,7 +431,7 @@ extract_kernel(ExtractArgs a) {
   // contiguous per wave.
   const int P = a.tab.P;
   const int64_t nkt = a.nkt;
-  const int64_t rt = rblk >> 4, fr = rblk & 15;
+  const int64_t rt = rblk >> 3, fr = (rblk & 7) * 2 + (wave & 1);
   const int64_t plane = isA ? a.planeA : a.planeB;
   int8_t* base = (isA ? a.planesA : a.planesB) + b * (isA ? a.memberA : a.memberB);
   const int64_t off = (rt * nkt + kt) * kTileBytes + fr * kFragBytes + lane * 16;
@@ -469,15 +473,19 @@ extract_kernel(ExtractArgs a) {
 // modulus slots (the reference's bal8, :613-620, here as an exact fp64
 // nearest-quotient reduction), raw int32 for correction slots.
 //
-// 4 waves in a 2x2 arrangement, 128x128 per wave = 8x8 MFMA 16x16x64 tiles
-// (256 accumulator registers), LDS double-buffered 32 KiB stages fed by
-// coalesced 16-byte loads of the fragment-ordered planes; fragment reads are
-// linear 16 B per lane, so they are bank-conflict free.
+// 4 waves in a 2x2 arrangement, 128x128 per wave = 4x4 v_mfma_i32_32x32x32_i8
+// tiles (256 accumulator registers).  Operand tiles stream into a 4-stage LDS
+// ring with direct global->LDS copies (prefetch distance 3 k-steps); the
+// planes are stored in fragment order, so each stage is a linear copy and
+// every fragment read is 16 contiguous bytes per lane (bank-conflict free).
+// Fragments are double-buffered in registers: while the MFMAs of k-step kt
+// run, the fragments of kt+1 are read, so LDS latency stays off the MFMA
+// path.  One explicit wait + barrier per k-step.
 //
-// Output blocks (res8 / corr planes): 16x16 blocks, row-block major; inside
-// a block lane l = 16 * (row / 4) + col holds rows 4*(l/16) + 0..3 of column
-// l % 16 -- the MFMA accumulator order -- as 4 consecutive bytes (int8) or
-// 4 consecutive int32.
+// Output blocks (res8 / corr planes): 32x32 blocks, row-block major; inside
+// a block, lane l holds 16 elements in the MFMA accumulator order --
+// element v of lane l is (row 8*(v/4) + 4*(l/32) + v%4, column l%32) -- as
+// 16 consecutive bytes (int8) or 16 consecutive int32.
 
 struct GemmArgs {
   const int8_t* A;
@@ -494,9 +502,36 @@ struct GemmArgs {
   double invp[kMaxP];
 };
 
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// s_waitcnt immediate (gfx9 encoding): wait until at most `vm` vector-memory
+// operations of this wave are outstanding and all LDS operations are done.
+template <int vm>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(vm >= 0 && vm < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((vm & 15) | (7 << 4) | (0 << 8) | ((vm >> 4) << 14));
+}
+
+// Work-group barrier without the release/acquire fences of __syncthreads(),
+// whose release half drains every outstanding vector-memory operation
+// (including the LDS prefetch ring).  Callers wait explicitly
+// (wait_vm_lgkm0) before it; the empty asm statements keep the compiler from
+// moving memory accesses across.
+__device__ __forceinline__ void barrier_lds() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) int8_t lds_i8;
+
+constexpr int kStages = 4;                   // LDS ring: 4 x 32 KiB
+constexpr int kStageBytes = 2 * kTileBytes;  // A tile then B tile
+constexpr int kDmaPerStep = 8;               // per wave: 4 KiB of A + 4 KiB of B
+
 __global__ void __launch_bounds__(kThreads, 1)
 modgemm_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) int8_t lds[2][2 * kTileBytes];
+  __shared__ __attribute__((aligned(1024))) int8_t lds[kStages * kStageBytes];
 
   // XCD-aware order: work group i runs on XCD i % 8.  Within each full chunk
   // of 256 groups, XCD x takes logical items 32x .. 32x+31, an 8x4 block of
@@ -526,100 +561,138 @@ modgemm_kernel(GemmArgs g) {
   const int kt0 = (is_corr && g.ncorr == 2) ? slot * g.nkt : 0;
   const int nk = is_corr ? (g.ncorr == 1 ? 2 * g.nkt : g.nkt) : g.nkt;
 
-  const v4i* __restrict__ At = reinterpret_cast<const v4i*>(
-      g.A + b * g.memberA + (int64_t)plane * g.planeA + ((int64_t)mt * rstride + kt0) * kTileBytes);
-  const v4i* __restrict__ Bt = reinterpret_cast<const v4i*>(
-      g.B + b * g.memberB + (int64_t)plane * g.planeB + ((int64_t)nt * rstride + kt0) * kTileBytes);
+  const int8_t* At = g.A + b * g.memberA + (int64_t)plane * g.planeA +
+                     ((int64_t)mt * rstride + kt0) * kTileBytes;
+  const int8_t* Bt = g.B + b * g.memberB + (int64_t)plane * g.planeB +
+                     ((int64_t)nt * rstride + kt0) * kTileBytes;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  constexpr int kV = kTileBytes / 16;   // v4i per operand tile (1024)
 
-  v4i acc[8][8];
-#pragma unroll
-  for (int x = 0; x < 8; ++x)
-#pragma unroll
-    for (int y = 0; y < 8; ++y) acc[x][y] = v4i{0, 0, 0, 0};
+  // Each wave copies fragments 4*wave .. 4*wave+3 of both operand tiles:
+  // the instruction offset advances the global and the LDS address alike.
+  const uint32_t goff = (uint32_t)(wave * 4096 + lane * 16);
+#define FP64EMU_ISSUE(kt)                                                              \
+  do {                                                                                 \
+    lds_i8* st_ = (lds_i8*)(lds + ((kt) & (kStages - 1)) * kStageBytes + wave * 4096); \
+    const int8_t* a_ = At + (int64_t)(kt) * kTileBytes + goff;                         \
+    const int8_t* b_ = Bt + (int64_t)(kt) * kTileBytes + goff;                         \
+    __builtin_amdgcn_global_load_lds(a_, st_, 16, 0, 0);                               \
+    __builtin_amdgcn_global_load_lds(a_, st_, 16, 1024, 0);                            \
+    __builtin_amdgcn_global_load_lds(a_, st_, 16, 2048, 0);                            \
+    __builtin_amdgcn_global_load_lds(a_, st_, 16, 3072, 0);                            \
+    __builtin_amdgcn_global_load_lds(b_, st_ + kTileBytes, 16, 0, 0);                  \
+    __builtin_amdgcn_global_load_lds(b_, st_ + kTileBytes, 16, 1024, 0);               \
+    __builtin_amdgcn_global_load_lds(b_, st_ + kTileBytes, 16, 2048, 0);               \
+    __builtin_amdgcn_global_load_lds(b_, st_ + kTileBytes, 16, 3072, 0);               \
+  } while (0)
+  // Fragments of one k-step: F[0..7] = A row blocks 4 wm .. 4 wm + 3 (both k
+  // halves), F[8..15] = the same for B.
+#define FP64EMU_READF(F, kt)                                                               \
+  do {                                                                                     \
+    const v4i* sa_ = reinterpret_cast<const v4i*>(lds + ((kt) & (kStages - 1)) * kStageBytes); \
+    const v4i* sb_ = sa_ + kTileBytes / 16;                                                \
+    _Pragma("unroll") for (int y = 0; y < 8; ++y) F[8 + y] = sb_[(wn * 8 + y) * 64 + lane]; \
+    _Pragma("unroll") for (int x = 0; x < 8; ++x) F[x] = sa_[(wm * 8 + x) * 64 + lane];     \
+  } while (0)
+#define FP64EMU_MMA(F)                                                                      \
+  do {                                                                                      \
+    _Pragma("unroll") for (int h = 0; h < 2; ++h)                                           \
+    _Pragma("unroll") for (int x = 0; x < 4; ++x)                                           \
+    _Pragma("unroll") for (int y = 0; y < 4; ++y)                                           \
+      acc[x][y] = __builtin_amdgcn_mfma_i32_32x32x32_i8(F[2 * x + h], F[8 + 2 * y + h],     \
+                                                         acc[x][y], 0, 0, 0);               \
+  } while (0)
+  // One k-step: stage kt+1 must have landed (own copies: at most one later
+  // group in flight), then the barrier makes every wave's copies visible
+  // and guarantees every wave finished reading the stage refilled next.
+#define FP64EMU_STEP(kt, FC, FN)                                                         \
+  do {                                                                                   \
+    if ((kt) + 3 <= nk) wait_vm_lgkm0<kDmaPerStep>(); else wait_vm_lgkm0<0>();           \
+    barrier_lds();                                                                       \
+    if ((kt) + 3 < nk) FP64EMU_ISSUE((kt) + 3);                                          \
+    FP64EMU_READF(FN, (kt) + 1);                                                         \
+    FP64EMU_MMA(FC);                                                                     \
+    _Pragma("unroll") for (int q = 0; q < 16; ++q) {                                     \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                 \
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                                 \
+    }                                                                                    \
+  } while (0)
 
-  v4i ra[4], rb[4];
+  v16i acc[4][4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 4; ++y) acc[x][y] = v16i{};
+
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s)
+    if (s < nk) FP64EMU_ISSUE(s);
+  v4i F0[16], F1[16];
   if (nk > 0) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      ra[u] = At[u * kThreads + tid];
-      rb[u] = Bt[u * kThreads + tid];
-    }
-    v4i* s0 = reinterpret_cast<v4i*>(lds[0]);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      s0[u * kThreads + tid] = ra[u];
-      s0[kV + u * kThreads + tid] = rb[u];
-    }
+    wait_vm_lgkm0<0>();
+    barrier_lds();
+    FP64EMU_READF(F0, 0);
   }
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
-    if (more) {
-      const v4i* an = At + (int64_t)(kt + 1) * kV;
-      const v4i* bn = Bt + (int64_t)(kt + 1) * kV;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        ra[u] = an[u * kThreads + tid];
-        rb[u] = bn[u * kThreads + tid];
-      }
-    }
-    const v4i* sa = reinterpret_cast<const v4i*>(lds[kt & 1]);
-    const v4i* sbp = sa + kV;
-    v4i af[8], bf[8];
-#pragma unroll
-    for (int x = 0; x < 8; ++x) af[x] = sa[(wm * 8 + x) * 64 + lane];
-#pragma unroll
-    for (int y = 0; y < 8; ++y) bf[y] = sbp[(wn * 8 + y) * 64 + lane];
-#pragma unroll
-    for (int x = 0; x < 8; ++x)
-#pragma unroll
-      for (int y = 0; y < 8; ++y)
-        acc[x][y] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[x], bf[y], acc[x][y], 0, 0, 0);
-    if (more) {
-      v4i* sn = reinterpret_cast<v4i*>(lds[(kt + 1) & 1]);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        sn[u * kThreads + tid] = ra[u];
-        sn[kV + u * kThreads + tid] = rb[u];
-      }
-    }
-    __syncthreads();
+  // Reading fragments of k-step nk (one past the end) touches a stale stage
+  // and is never used; no copy targets it.
+  int kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    FP64EMU_STEP(kt, F0, F1);
+    FP64EMU_STEP(kt + 1, F1, F0);
   }
+  if (kt < nk) {
+    wait_vm_lgkm0<0>();
+    FP64EMU_MMA(F0);
+  }
+  // No copy may still target this work group's LDS when it retires.
+  wait_vm_lgkm0<0>();
+#undef FP64EMU_ISSUE
+#undef FP64EMU_READF
+#undef FP64EMU_MMA
+#undef FP64EMU_STEP
 
-  // Epilogue.
-  const int64_t NB = (int64_t)g.TN * 16;              // 16-blocks per output row
-  const int64_t mb0 = (int64_t)mt * 16 + wm * 8, nb0 = (int64_t)nt * 16 + wn * 8;
+  // Epilogue: 32x32 blocks (mb, nb) of this wave, 16 values per lane.
+  const int64_t NB = (int64_t)g.TN * 8;                 // 32-blocks per output row
+  const int64_t mb0 = (int64_t)mt * 8 + wm * 4, nb0 = (int64_t)nt * 8 + wn * 4;
   if (is_corr) {
     int32_t* dst = g.corr + (b * g.ncorr + slot) * g.outplane;
 #pragma unroll
-    for (int x = 0; x < 8; ++x)
+    for (int x = 0; x < 4; ++x)
 #pragma unroll
-      for (int y = 0; y < 8; ++y)
-        *reinterpret_cast<v4i*>(dst + ((mb0 + x) * NB + nb0 + y) * kOutBlkBytes + lane * 4) =
-            acc[x][y];
+      for (int y = 0; y < 4; ++y) {
+        v4i* d = reinterpret_cast<v4i*>(dst + ((mb0 + x) * NB + nb0 + y) * 1024 + lane * 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          d[q] = v4i{acc[x][y][4 * q], acc[x][y][4 * q + 1], acc[x][y][4 * q + 2], acc[x][y][4 * q + 3]};
+        __builtin_amdgcn_sched_barrier(0);
+      }
   } else {
     const int t = plane;
     const double pd = (double)g.p[t], ip = g.invp[t];
     int8_t* dst = g.res8 + (b * g.P + t) * g.outplane;
 #pragma unroll
-    for (int x = 0; x < 8; ++x)
+    for (int x = 0; x < 4; ++x)
 #pragma unroll
-      for (int y = 0; y < 8; ++y) {
-        uint32_t w = 0u;
+      for (int y = 0; y < 4; ++y) {
+        uint32_t w[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          // |acc| < 2^31: the nearest quotient is exact (see extraction).
-          const double av = (double)acc[x][y][v];
-          const double q = fma(av, ip, kMagic) - kMagic;
-          const int rr = (int)fma(-q, pd, av);
-          w |= ((uint32_t)rr & 0xFFu) << (8 * v);
+        for (int q = 0; q < 4; ++q) {
+          uint32_t u = 0u;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            // |acc| < 2^31: the nearest quotient is exact (see extraction).
+            const double av = (double)acc[x][y][4 * q + v];
+            const double qq = fma(av, ip, kMagic) - kMagic;
+            const int rr = (int)fma(-qq, pd, av);
+            u |= ((uint32_t)rr & 0xFFu) << (8 * v);
+          }
+          w[q] = u;
         }
-        *reinterpret_cast<uint32_t*>(dst + ((mb0 + x) * NB + nb0 + y) * kOutBlkBytes + lane * 4) = w;
+        *reinterpret_cast<v4i*>(dst + ((mb0 + x) * NB + nb0 + y) * 1024 + lane * 16) =
+            v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        __builtin_amdgcn_sched_barrier(0);
       }
   }
 }
@@ -631,7 +704,10 @@ modgemm_kernel(GemmArgs g) {
 // Horner per group of 7 moduli; exact: 128-bit a0 + M0 (a1 + M1 a2) plus the
 // correction (corr1 + corr2) << (be - 15), correctly rounded to double, then
 // ldexp by -(sftA + sftB).  fp64_emu_cuda/fp64_emu.cu:849-952 and the s128
-// helpers :53-105.  One wave per 16x16 output block, 4 elements per lane.
+// helpers :53-105.  One work group per 32x32 output block: thread t reads
+// dword t of each blocked plane (lane t/4 of the GEMM's accumulator order,
+// elements 4*(t%4) .. +3), i.e. rows 8*(t%4) + 4*(t/128) + 0..3 of column
+// (t/4)%32 -- coalesced loads, 4 elements per thread.
 
 struct s128v {
   uint64_t lo;
@@ -693,8 +769,8 @@ struct ReconArgs {
   const int16_t* sftB;
   const int* bits_eff;
   int64_t M, N, batch, outplane;
-  int64_t NB;          // 16-blocks per padded output row (Np / 16)
-  int64_t MBv, NBv;    // 16-blocks covering the valid M, N
+  int64_t NB;          // 32-blocks per padded output row (Np / 32)
+  int64_t MBv, NBv;    // 32-blocks covering the valid M, N
   int64_t nblocks;     // batch * MBv * NBv
   int ncorr;
   ModTables tab;
@@ -703,24 +779,25 @@ struct ReconArgs {
 template <bool kExact>
 __global__ void __launch_bounds__(kThreads)
 reconstruct_kernel(ReconArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t wv = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  if (wv >= a.nblocks) return;
+  const int64_t blk = blockIdx.x;
+  if (blk >= a.nblocks) return;
+  const int t = threadIdx.x;
   const int64_t per = a.MBv * a.NBv;
-  const int64_t b = wv / per;
-  const int64_t rem = wv - b * per;
+  const int64_t b = blk / per;
+  const int64_t rem = blk - b * per;
   const int64_t mb = rem / a.NBv, nb = rem - (rem / a.NBv) * a.NBv;
-  const int64_t i0 = mb * 16 + 4 * (lane >> 4);
-  const int64_t j = nb * 16 + (lane & 15);
+  const int l = t >> 2, q = t & 3;
+  const int64_t i0 = mb * 32 + 8 * q + 4 * (l >> 5);
+  const int64_t j = nb * 32 + (l & 31);
   if (j >= a.N || i0 >= a.M) return;
 
   const int P = a.tab.P;
-  const int64_t boff = (mb * a.NB + nb) * kOutBlkBytes + lane * 4;
+  const int64_t boff = (mb * a.NB + nb) * 1024 + 4 * t;   // byte offset (int8) / element (int32)
   uint32_t w[kMaxP];
 #pragma unroll
-  for (int t = 0; t < kMaxP; ++t) {
-    if (t >= P) break;
-    w[t] = *reinterpret_cast<const uint32_t*>(a.res8 + (b * P + t) * a.outplane + boff);
+  for (int tt = 0; tt < kMaxP; ++tt) {
+    if (tt >= P) break;
+    w[tt] = *reinterpret_cast<const uint32_t*>(a.res8 + (b * P + tt) * a.outplane + boff);
   }
   int64_t cv[4] = {0, 0, 0, 0};
   if (a.ncorr > 0) {
@@ -977,12 +1054,12 @@ int run(const Call& c) {
     ra.res8 = res8; ra.corr = corr; ra.out = c.out;
     ra.sftA = sftA; ra.sftB = sftB; ra.bits_eff = bits_eff;
     ra.M = c.M; ra.N = c.N; ra.batch = c.batch; ra.outplane = L.outplane_bytes;
-    ra.NB = L.Np / 16;
-    ra.MBv = (c.M + 15) / 16; ra.NBv = (c.N + 15) / 16;
+    ra.NB = L.Np / 32;
+    ra.MBv = (c.M + 31) / 32; ra.NBv = (c.N + 31) / 32;
     ra.nblocks = c.batch * ra.MBv * ra.NBv;
     ra.ncorr = L.ncorr;
     ra.tab = tab;
-    const unsigned grid = (unsigned)((ra.nblocks + 3) / 4);
+    const unsigned grid = (unsigned)ra.nblocks;
     if (c.exact)
       hipLaunchKernelGGL(reconstruct_kernel<true>, dim3(grid), dim3(kThreads), 0, s, ra);
     else
