@@ -700,54 +700,28 @@ modgemm_kernel(GemmArgs g) {
 // ---------------------------------------------------------------------------
 // Reconstruction.  Per output element: balanced Garner digits
 //   d_t = bal((r_t - sum_{u<t} d_u (M_u mod p_t)) (M_t mod p_t)^-1 mod p_t)
-// with the O(P^2) inner products as v_dot4_i32_i8 over packed digits; int64
-// Horner per group of 7 moduli; exact: 128-bit a0 + M0 (a1 + M1 a2) plus the
-// correction (corr1 + corr2) << (be - 15), correctly rounded to double, then
-// ldexp by -(sftA + sftB).  fp64_emu_cuda/fp64_emu.cu:849-952 and the s128
-// helpers :53-105.  One work group per 32x32 output block: thread t reads
-// dword t of each blocked plane (lane t/4 of the GEMM's accumulator order,
-// elements 4*(t%4) .. +3), i.e. rows 8*(t%4) + 4*(t/128) + 0..3 of column
-// (t/4)%32 -- coalesced loads, 4 elements per thread.
+// with the O(P^2) inner products as v_dot4_i32_i8 over packed digits; Horner
+// per group of 7 moduli (the first four steps of a group in int32: a balanced
+// mixed-radix value of four digits is below 2^31); exact: 128-bit
+// a0 + M0 (a1 + M1 a2) plus the correction (corr1 + corr2) << (be - 15),
+// correctly rounded to double, then ldexp by -(sftA + sftB).
+// fp64_emu_cuda/fp64_emu.cu:849-952 and the s128 helpers :53-105.
+//
+// One work group per 32x32 output block: thread t reads dword t of each
+// blocked plane (lane t/4 of the GEMM's accumulator order, elements
+// 4*(t%4) .. +3), i.e. rows 8*(t%4) + 4*(t/128) + 0..3 of column (t/4)%32 --
+// coalesced loads, 4 elements per thread, processed in lockstep so each
+// modulus constant is used four times right after its scalar load.
 
-struct s128v {
-  uint64_t lo;
-  int64_t hi;
-};
-
-__device__ __forceinline__ s128v s128_of(int64_t v) {
-  return s128v{(uint64_t)v, v < 0 ? -1ll : 0ll};
-}
-
-// a * m + d, m < 2^57 positive, d signed 64-bit; exact while |a*m| < 2^126.
-__device__ __forceinline__ s128v s128_fma64(s128v a, uint64_t m, int64_t d) {
-  const uint64_t lo = a.lo * m;
-  const int64_t hi = (int64_t)__umul64hi(a.lo, m) + a.hi * (int64_t)m;
-  s128v r;
-  r.lo = lo + (uint64_t)d;
-  r.hi = hi + (r.lo < lo ? 1 : 0) + (d < 0 ? -1 : 0);
-  return r;
-}
-
-__device__ __forceinline__ s128v s128_add_shl(s128v a, int64_t c, int s) {
-  // a + c * 2^s for 0 < s < 64.
-  const uint64_t clo = (uint64_t)c << s;
-  const int64_t chi = (int64_t)(((uint64_t)(c < 0 ? -1ll : 0ll) << s) | ((uint64_t)c >> (64 - s)));
-  s128v r;
-  r.lo = a.lo + clo;
-  r.hi = a.hi + chi + (r.lo < clo ? 1 : 0);
-  return r;
-}
+typedef __int128 i128;
 
 // Round-to-nearest-even conversion of a signed 128-bit integer: the top 64
 // significant bits with the dropped tail as a sticky bit (11 positions below
 // the rounding point) convert once.
-__device__ __forceinline__ double s128_to_f64(s128v a) {
-  const bool neg = a.hi < 0;
-  uint64_t lo = a.lo, hi = (uint64_t)a.hi;
-  if (neg) {
-    lo = ~lo + 1ull;
-    hi = ~hi + (lo == 0ull ? 1ull : 0ull);
-  }
+__device__ __forceinline__ double i128_to_f64(i128 v) {
+  const bool neg = v < 0;
+  const unsigned __int128 u = neg ? (unsigned __int128)(-v) : (unsigned __int128)v;
+  const uint64_t hi = (uint64_t)(u >> 64), lo = (uint64_t)u;
   double m;
   if (hi == 0ull) {
     m = (double)lo;
@@ -781,88 +755,131 @@ __global__ void __launch_bounds__(kThreads)
 reconstruct_kernel(ReconArgs a) {
   const int64_t blk = blockIdx.x;
   if (blk >= a.nblocks) return;
-  const int t = threadIdx.x;
+  const int thr = threadIdx.x;
   const int64_t per = a.MBv * a.NBv;
   const int64_t b = blk / per;
   const int64_t rem = blk - b * per;
   const int64_t mb = rem / a.NBv, nb = rem - (rem / a.NBv) * a.NBv;
-  const int l = t >> 2, q = t & 3;
-  const int64_t i0 = mb * 32 + 8 * q + 4 * (l >> 5);
+  const int l = thr >> 2, q4 = thr & 3;
+  const int64_t i0 = mb * 32 + 8 * q4 + 4 * (l >> 5);
   const int64_t j = nb * 32 + (l & 31);
   if (j >= a.N || i0 >= a.M) return;
 
   const int P = a.tab.P;
-  const int64_t boff = (mb * a.NB + nb) * 1024 + 4 * t;   // byte offset (int8) / element (int32)
+  const int64_t boff = (mb * a.NB + nb) * 1024 + 4 * thr;  // byte (int8) / element (int32)
   uint32_t w[kMaxP];
 #pragma unroll
-  for (int tt = 0; tt < kMaxP; ++tt) {
-    if (tt >= P) break;
-    w[tt] = *reinterpret_cast<const uint32_t*>(a.res8 + (b * P + tt) * a.outplane + boff);
-  }
+  for (int t = 0; t < kMaxP; ++t)
+    if (t < P) w[t] = *reinterpret_cast<const uint32_t*>(a.res8 + (b * P + t) * a.outplane + boff);
   int64_t cv[4] = {0, 0, 0, 0};
   if (a.ncorr > 0) {
     const v4i c1 = *reinterpret_cast<const v4i*>(a.corr + (b * a.ncorr) * a.outplane + boff);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) cv[v] = c1[v];
+    for (int e = 0; e < 4; ++e) cv[e] = c1[e];
     if (a.ncorr == 2) {
       const v4i c2 = *reinterpret_cast<const v4i*>(a.corr + (b * a.ncorr + 1) * a.outplane + boff);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) cv[v] += c2[v];
+      for (int e = 0; e < 4; ++e) cv[e] += c2[e];
     }
   }
+
+  // Garner digits, 4 elements in lockstep.
+  int dg[4][kMaxP];
+  int dp[4][kGarnerWords];
+  int pv[kMaxP];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int g = 0; g < kGarnerWords; ++g) dp[e][g] = 0;
+#pragma unroll
+  for (int t = 0; t < kMaxP; ++t) {
+    if (t >= P) continue;
+    const int pt = a.tab.p[t];
+    pv[t] = pt;
+    if (t == 0) {
+      // M_0 = 1: the first digit is the (balanced) residue itself.
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = (int)(int8_t)(uint8_t)(w[0] >> (8 * e));
+        dg[e][0] = d;
+        dp[e][0] = (int)((uint32_t)d & 0xFFu);
+      }
+      continue;
+    }
+    const int mi = a.tab.minv[t];
+    const double pd = (double)pt, ip = a.tab.invp[t];
+    int mpw[kGarnerWords];
+#pragma unroll
+    for (int g = 0; g < kGarnerWords; ++g) mpw[g] = (4 * g < t) ? a.tab.mp[t * kGarnerWords + g] : 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int rt = (int)(int8_t)(uint8_t)(w[t] >> (8 * e));
+      int acc = 0;                                      // |acc| < 19 * 128 * 128 < 2^19
+#pragma unroll
+      for (int g = 0; g < kGarnerWords; ++g)
+        if (4 * g < t) acc = __builtin_amdgcn_sdot4(dp[e][g], mpw[g], acc, false);
+      const double yd = (double)__mul24(rt - acc, mi);  // |y| < 2^27, 24-bit operands
+      const double qq = fma(yd, ip, kMagic) - kMagic;   // exact nearest quotient
+      dg[e][t] = (int)fma(-qq, pd, yd);
+    }
+    // Even modulus (uniform branch): the nearest quotient can leave +p/2,
+    // whose balanced representative is -p/2.
+    if ((pt & 1) == 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (dg[e][t] == (pt >> 1)) dg[e][t] -= pt;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      dp[e][t >> 2] |= (int)(((uint32_t)dg[e][t] & 0xFFu) << (8 * (t & 3)));
+  }
+
+  // Horner per group of 7 (digits 7g .. 7g+6, high to low): group position
+  // 6..3 in int32 (four balanced digits stay below 2^31; three below 2^23,
+  // so the 24-bit multiply is exact), positions 2..0 in int64.
+  int h32[4][3];
+  long long ag[4][3];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int g = 0; g < 3; ++g) { h32[e][g] = 0; ag[e][g] = 0; }
+#pragma unroll
+  for (int t = kMaxP - 1; t >= 0; --t) {
+    if (t >= P) continue;
+    const int g = t / 7, pos = t % 7;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (pos >= 3) h32[e][g] = __mul24(h32[e][g], pv[t]) + dg[e][t];
+      else if (pos == 2) ag[e][g] = (long long)h32[e][g] * pv[t] + dg[e][t];
+      else ag[e][g] = ag[e][g] * pv[t] + dg[e][t];
+    }
+  }
+
   const int cshift = a.bits_eff[0] - 15;
   const int sj = (int)a.sftB[b * a.N + j];
   const int ng = (P + 6) / 7;
-
-  for (int v = 0; v < 4; ++v) {
-    const int64_t i = i0 + v;
-    if (i >= a.M) break;
-    int dp[kGarnerWords] = {0, 0, 0, 0, 0};
-    int dg[kMaxP];
 #pragma unroll
-    for (int t = 0; t < kMaxP; ++t) {
-      if (t >= P) continue;
-      const int rt = (int)(int8_t)(uint8_t)(w[t] >> (8 * v));
-      int d;
-      if (t == 0) {
-        d = rt;   // M_0 = 1: the first digit is the (balanced) residue
-      } else {
-        int acc = 0;
+  for (int e = 0; e < 4; ++e) {
+    const int64_t i = i0 + e;
+    if (i >= a.M) continue;
+    // A group with fewer than 3 digits never reached its int64 steps.
+    long long gv[3];
 #pragma unroll
-        for (int gw = 0; gw < kGarnerWords; ++gw)
-          if (4 * gw < t) acc = __builtin_amdgcn_sdot4(dp[gw], a.tab.mp[t * kGarnerWords + gw], acc, false);
-        const int y = (rt - acc) * a.tab.minv[t];      // |y| < 2^27
-        const double yd = (double)y;
-        const double q = fma(yd, a.tab.invp[t], kMagic) - kMagic;
-        d = (int)fma(-q, (double)a.tab.p[t], yd);
-        // Even modulus: the nearest quotient can leave +p/2; balanced is -p/2.
-        if ((a.tab.p[t] & 1) == 0 && d == a.tab.p[t] / 2) d -= a.tab.p[t];
-      }
-      dg[t] = d;
-      dp[t >> 2] |= (int)(((uint32_t)d & 0xFFu) << (8 * (t & 3)));
-    }
-    long long a0 = 0, a1 = 0, a2 = 0;
-#pragma unroll
-    for (int t = kMaxP - 1; t >= 0; --t) {
-      if (t >= P) continue;
-      const long long d = dg[t];
-      if (t >= 14) a2 = a2 * a.tab.p[t] + d;
-      else if (t >= 7) a1 = a1 * a.tab.p[t] + d;
-      else a0 = a0 * a.tab.p[t] + d;
-    }
+    for (int g = 0; g < 3; ++g) gv[g] = (P > 7 * g + 2) ? ag[e][g] : (long long)h32[e][g];
+    const long long a0 = gv[0], a1 = gv[1], a2 = gv[2];
     const int sh = -((int)a.sftA[b * a.M + i] + sj);
     double val;
     if (kExact) {
-      s128v acc = s128_of(ng == 3 ? a2 : (ng == 2 ? a1 : a0));
-      if (ng == 3) acc = s128_fma64(acc, (uint64_t)a.tab.m64[1], a1);
-      if (ng >= 2) acc = s128_fma64(acc, (uint64_t)a.tab.m64[0], a0);
-      if (cv[v] != 0) acc = s128_add_shl(acc, cv[v], cshift);
-      val = s128_to_f64(acc);
+      i128 acc = ng == 3 ? (i128)a2 : (ng == 2 ? (i128)a1 : (i128)a0);
+      if (ng == 3) acc = acc * (i128)(uint64_t)a.tab.m64[1] + a1;
+      if (ng >= 2) acc = acc * (i128)(uint64_t)a.tab.m64[0] + a0;
+      acc += (i128)cv[e] * ((i128)1 << cshift);
+      val = i128_to_f64(acc);
     } else {
       double acc = (double)(ng == 3 ? a2 : (ng == 2 ? a1 : a0));
       if (ng == 3) acc = fma(acc, (double)a.tab.m64[1], (double)a1);
       if (ng >= 2) acc = fma(acc, (double)a.tab.m64[0], (double)a0);
-      acc = acc + ldexp((double)cv[v], cshift);
+      acc = acc + ldexp((double)cv[e], cshift);
       val = acc;
     }
     a.out[(b * a.M + i) * a.N + j] = ldexp(val, sh);
