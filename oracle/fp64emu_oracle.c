@@ -492,3 +492,38 @@ void or_ddgemm_nt(double* hi, double* lo, const double* A, const double* Bt, int
     }
   (void)nthreads;
 }
+
+/* ---- array forms of the scalar restatements (for exhaustive pinning) ---- */
+
+void or_bal8_array(const int32_t* v, int64_t n, int p, int8_t* out) {
+  for (int64_t i = 0; i < n; i++) out[i] = or_bal8(v[i], p);
+}
+
+void or_barrett_bal32_array(const int32_t* y, int64_t n, int p, int32_t* out) {
+  const uint32_t mu32 = (uint32_t)((1u << 31) / (unsigned)p);
+  for (int64_t i = 0; i < n; i++) out[i] = or_barrett_bal32(y[i], p, mu32, (uint32_t)p << 21);
+}
+
+/* Extraction of n elements with per-element shifts: td (the signed scaled
+ * integer), balanced residues res[n][P], hi7/q7. */
+void or_extract_array(const double* x, const int32_t* shift, int64_t n, int bits_eff,
+                      const int32_t* primes, int P, int64_t* td, int8_t* res, int8_t* hi,
+                      int8_t* q) {
+  for (int64_t i = 0; i < n; i++) {
+    int8_t h = 0, qq = 0;
+    const uint64_t uu = or_split(x[i], shift[i], bits_eff, 1, &h, &qq);
+    td[i] = (int64_t)(uu - ((uint64_t)1 << bits_eff));
+    for (int t = 0; t < P; t++) res[i * P + t] = or_residue(uu, primes[t], bits_eff);
+    hi[i] = h;
+    q[i] = qq;
+  }
+}
+
+/* Correctly rounded conversion of n signed 128-bit integers given as
+ * (hi, lo) 64-bit halves. */
+void or_i128_array_to_double(const int64_t* hi, const uint64_t* lo, int64_t n, double* out) {
+  for (int64_t i = 0; i < n; i++) {
+    const i128 v = (i128)(((unsigned __int128)(uint64_t)hi[i] << 64) | lo[i]);
+    out[i] = or_i128_to_double(v);
+  }
+}

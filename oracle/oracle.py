@@ -85,6 +85,10 @@ def lib():
         L.or_mm.restype = i32
         L.or_ddgemm_nt.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32]
         L.or_i128_to_double.restype = ctypes.c_double
+        L.or_bal8_array.argtypes = [vp, i64, i32, vp]
+        L.or_barrett_bal32_array.argtypes = [vp, i64, i32, vp]
+        L.or_extract_array.argtypes = [vp, vp, i64, i32, vp, i32, vp, vp, vp, vp]
+        L.or_i128_array_to_double.argtypes = [vp, vp, i64, vp]
         _LIB = L
     return _LIB
 
@@ -166,6 +170,46 @@ def extract_operand(X, kn, sft, bits_eff, primes, do_corr=True):
     lib().or_extract_operand(_p(X), batch, R, K, int(kn), _p(sft), int(bits_eff), _p(primes), P,
                              int(do_corr), _p(res), _p(hi), _p(q))
     return res, hi, q
+
+
+def bal8_array(v, p):
+    """The GEMM epilogue's 31-bit Barrett (fp64_emu.cu:613-620) on an int32 array."""
+    v = _c(v, np.int32)
+    out = np.zeros(v.shape, np.int8)
+    lib().or_bal8_array(_p(v), v.size, int(p), _p(out))
+    return out
+
+
+def barrett_bal32_array(y, p):
+    """barrett_bal32 (fp64_emu.cu:42-51) with the Garner bias p << 21."""
+    y = _c(y, np.int32)
+    out = np.zeros(y.shape, np.int32)
+    lib().or_barrett_bal32_array(_p(y), y.size, int(p), _p(out))
+    return out
+
+
+def extract_array(x, shift, bits_eff, primes):
+    """Per-element extraction: (td int64, res [n, P] int8, hi int8, q int8)."""
+    x = _c(x, np.float64).ravel()
+    shift = _c(np.broadcast_to(np.asarray(shift, np.int32), x.shape), np.int32)
+    primes = _c(primes, np.int32)
+    n, P = x.size, primes.size
+    td = np.zeros(n, np.int64)
+    res = np.zeros((n, P), np.int8)
+    hi = np.zeros(n, np.int8)
+    q = np.zeros(n, np.int8)
+    lib().or_extract_array(_p(x), _p(shift), n, int(bits_eff), _p(primes), P, _p(td), _p(res),
+                           _p(hi), _p(q))
+    return td, res, hi, q
+
+
+def i128_to_double(values):
+    """Correctly rounded conversion of Python ints in the signed 128-bit range."""
+    hi = np.array([(v >> 64) for v in values], dtype=np.int64)
+    lo = np.array([v & ((1 << 64) - 1) for v in values], dtype=np.uint64)
+    out = np.zeros(len(values), np.float64)
+    lib().or_i128_array_to_double(_p(hi), _p(lo), len(values), _p(out))
+    return out
 
 
 def modgemm(A8, B8, p, nthreads=0):

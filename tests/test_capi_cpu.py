@@ -1,0 +1,217 @@
+"""CPU tier: the drop-in boundary without a GPU.
+
+- libfp64emu.so loads and exports every function include/fp64emu.h declares;
+- the workspace map is consistent (padding, alignment, no overlap, sizes);
+- argument validation returns the documented error codes and messages before
+  any device work (so it runs here, with no GPU);
+- the torch op library registers the reference's schemas verbatim
+  (torch-ext/torch_binding.cpp:7-12) with CUDA-only kernels: CPU tensors are
+  refused, never computed on a fallback;
+- the package refuses to import when the extension is not built.
+"""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fp64emu.h")
+
+torch = pytest.importorskip("torch")
+fp64_emu = pytest.importorskip("fp64_emu")
+from fp64_emu import capi  # noqa: E402
+
+EINVAL, EWORKSPACE = 1, 2
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b(fp64emu_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_exactly_the_exported_api():
+    declared = _declared_functions()
+    assert declared == sorted(capi.EXPORTS)
+    text = open(HEADER).read()
+    assert "extern \"C\"" in text
+    code = re.sub(r"//[^\n]*", "", re.sub(r"/\*.*?\*/", "", text, flags=re.S))
+    for torch_type in ("Tensor", "at::", "c10", "torch"):
+        assert torch_type not in code, torch_type   # plain pointers and sizes only
+
+
+def test_library_exports_every_declared_symbol():
+    L = ctypes.CDLL(capi.CAPI_PATH)
+    for name in _declared_functions():
+        assert hasattr(L, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", capi.CAPI_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    syms = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    for name in _declared_functions():
+        assert name in syms, name
+
+
+def test_maxp_and_status_codes():
+    L = capi.lib()
+    assert L.fp64emu_maxp() == 20
+    text = open(HEADER).read()
+    for name, val in (("FP64EMU_OK", 0), ("FP64EMU_EINVAL", 1), ("FP64EMU_EWORKSPACE", 2),
+                      ("FP64EMU_EHIP", 3)):
+        assert re.search(rf"{name}\s*=\s*{val}\b", text), name
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1, 1), (1, 128, 128, 4096), (1, 1023, 2049, 32769),
+                                   (64, 512, 512, 512), (1, 300, 7, 65537), (3, 0, 5, 10),
+                                   (1, 8192, 8192, 8192)])
+@pytest.mark.parametrize("P,corr", [(14, True), (13, False), (20, True)])
+def test_layout_consistency(shape, P, corr):
+    batch, M, N, K = shape
+    L = capi.layout(batch, M, N, K, P, corr)
+    assert L.Mp % 256 == 0 and L.Np % 256 == 0 and L.Kp % 64 == 0
+    assert L.Mp >= max(M, 1) and L.Mp - max(M, 1) < 256
+    assert L.Np >= max(N, 1) and L.Np - max(N, 1) < 256
+    assert L.Kp >= K and L.Kp - K < 64
+    assert L.ncorr == (0 if not corr else (1 if K <= 65536 else 2))
+    nplanes = P + (2 if corr else 0)
+    assert L.planeA_bytes == L.Mp * L.Kp and L.planeB_bytes == L.Np * L.Kp
+    assert L.memberA_bytes == nplanes * L.planeA_bytes
+    assert L.memberB_bytes == nplanes * L.planeB_bytes
+    assert L.outplane_bytes == L.Mp * L.Np
+    sizes = [("off_sftA", 2 * batch * M), ("off_sftB", 2 * batch * N), ("off_lgA", 4 * batch * M),
+             ("off_lgB", 4 * batch * N), ("off_bits", 16), ("off_pmax", 8 * L.nslab * batch * N),
+             ("off_pss", 8 * L.nslab * batch * N), ("off_planesA", batch * L.memberA_bytes),
+             ("off_planesB", batch * L.memberB_bytes), ("off_res8", batch * P * L.outplane_bytes),
+             ("off_corr", 4 * batch * L.ncorr * L.outplane_bytes)]
+    prev_end = 0
+    for name, size in sizes:
+        off = getattr(L, name)
+        assert off % 256 == 0, name
+        assert off >= prev_end, name
+        prev_end = off + size
+    assert L.total >= prev_end
+    assert capi.workspace_size(batch, M, N, K, P, corr) == L.total
+
+
+def test_layout_rejects_bad_arguments():
+    with pytest.raises(capi.CapiError):
+        capi.layout(1, -1, 4, 4, 14, True)
+    with pytest.raises(capi.CapiError):
+        capi.layout(1, 4, 4, 4, 21, True)
+    assert capi.workspace_size(1, 4, 4, 4, 0, True) == 0
+    assert capi.workspace_size(1, 4, 4, 4, 21, True) == 0
+
+
+def _call(kind="mm_nt", M=8, N=8, K=16, primes=None, bits=53, ws_bytes=None, null_ops=False,
+          batch=1):
+    """Invoke a C entry point with host-side dummies; every case here fails
+    validation (or is empty) before any pointer is dereferenced or any HIP
+    call is made."""
+    L = capi.lib()
+    pr = np.asarray(capi_primes(14) if primes is None else primes, np.int32)
+    pp = pr.ctypes.data_as(ctypes.c_void_p)
+    dummy = None if null_ops else ctypes.c_void_p(0x1000)
+    ws_size = capi.workspace_size(batch, max(M, 0), max(N, 0), max(K, 0), max(1, min(pr.size, 20)),
+                                  True)
+    ws_bytes = ws_size if ws_bytes is None else ws_bytes
+    ws = ctypes.c_void_p(0x2000)
+    if kind in ("mm", "mm_nt"):
+        st = getattr(L, "fp64emu_" + kind)(dummy, dummy, dummy, M, N, K, pp, None, None, pr.size, 1,
+                                           bits, 1, ws, ws_bytes, None)
+    else:
+        st = getattr(L, "fp64emu_" + kind)(dummy, dummy, dummy, batch, M, N, K, pp, None, None,
+                                           pr.size, 1, bits, 1, ws, ws_bytes, None)
+    return st, L.fp64emu_last_error().decode()
+
+
+def capi_primes(n):
+    return fp64_emu._PRIMES[:n]
+
+
+@pytest.mark.parametrize("kind", ["mm", "mm_nt", "bmm", "bmm_nt"])
+def test_validation_messages(kind):
+    assert _call(kind, bits=15) == (EINVAL, "bits must be in [16, 53]")
+    assert _call(kind, bits=54) == (EINVAL, "bits must be in [16, 53]")
+    assert _call(kind, primes=list(range(2, 23))) == (EINVAL, "too many primes")
+    assert _call(kind, primes=[256, 128]) == (EINVAL, "moduli must be pairwise coprime")
+    assert _call(kind, primes=[257, 255]) == (EINVAL, "moduli must be in [2, 256]")
+    assert _call(kind, primes=[1]) == (EINVAL, "moduli must be in [2, 256]")
+    assert _call(kind, K=131072) == (EINVAL, "K bound for int32 modular GEMM")
+    assert _call(kind, M=-1) == (EINVAL, "shapes must be non-negative")
+    assert _call(kind, ws_bytes=100) == (EWORKSPACE, "workspace too small")
+    assert _call(kind, null_ops=True)[0] == EINVAL
+
+
+def test_empty_shapes_are_a_no_op():
+    assert _call("mm_nt", M=0)[0] == 0
+    assert _call("mm", N=0)[0] == 0
+    assert _call("bmm_nt", batch=0)[0] == 0
+
+
+def test_torch_schemas_match_reference():
+    """The reference's op definitions (torch-ext/torch_binding.cpp:7-12),
+    parsed, equal the registered schemas."""
+    ref = [
+        "fp64_emu_mm(Tensor! out, Tensor A, Tensor B, Tensor primes_cpu, Tensor inv_cpu, Tensor mu_cpu, bool exact, int bits=53, bool use_corr=True) -> ()",
+        "fp64_emu_bmm(Tensor! out, Tensor A, Tensor B, Tensor primes_cpu, Tensor inv_cpu, Tensor mu_cpu, bool exact, int bits=53, bool use_corr=True) -> ()",
+        "fp64_emu_mm_nt(Tensor! out, Tensor A, Tensor Bt, Tensor primes_cpu, Tensor inv_cpu, Tensor mu_cpu, bool exact, int bits=53, bool use_corr=True) -> ()",
+        "fp64_emu_bmm_nt(Tensor! out, Tensor A, Tensor Bt, Tensor primes_cpu, Tensor inv_cpu, Tensor mu_cpu, bool exact, int bits=53, bool use_corr=True) -> ()",
+        "fp64_emu_mm_timed(Tensor! out, Tensor! times, Tensor A, Tensor B, Tensor primes_cpu, Tensor inv_cpu, Tensor mu_cpu, bool exact, int bits=53, bool use_corr=True) -> ()",
+        "fp64_emu_maxp() -> int",
+    ]
+    for d in ref:
+        name = d.split("(")[0]
+        want = torch._C.parse_schema("fp64_emu::" + d)
+        got = getattr(torch.ops.fp64_emu, name).default._schema
+        assert str(got) == str(want), name
+    assert torch.ops.fp64_emu.fp64_emu_maxp() == 20
+
+
+def test_fakes_registered_for_compile():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        primes = torch.tensor(capi_primes(14), dtype=torch.int32)
+        A = torch.empty(4, 8, dtype=torch.float64, device="cuda")
+        B = torch.empty(6, 8, dtype=torch.float64, device="cuda")
+        out = torch.empty(4, 6, dtype=torch.float64, device="cuda")
+        torch.ops.fp64_emu.fp64_emu_mm_nt(out, A, B, primes, primes, primes, True, 53, True)
+
+
+def test_cpu_tensors_are_refused_not_computed():
+    """The product has no CPU path: host tensors hit no kernel."""
+    A = torch.randn(4, 8, dtype=torch.float64)
+    B = torch.randn(6, 8, dtype=torch.float64)
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        fp64_emu.mm(A, B)                       # B as [N, K]
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        fp64_emu.mm_nt(A, B.T.contiguous())     # Bt as [K, N]
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        fp64_emu.bmm(A[None], B[None])
+
+
+def test_python_api_surface_mirrors_reference():
+    """torch-ext/fp64_emu/__init__.py: mm_nt, mm, bmm_nt, bmm, plan_config,
+    mm_timed (+ plan, range_bits helpers)."""
+    for name in ("mm_nt", "mm", "bmm_nt", "bmm", "plan_config", "mm_timed", "plan", "range_bits"):
+        assert callable(getattr(fp64_emu, name)), name
+    assert fp64_emu.plan_config(8192) == (14, True)
+    assert fp64_emu.plan_config(32769) == (15, True)
+
+
+def test_import_fails_loudly_without_extension(tmp_path):
+    """A copy of the package without the built .so files must not import."""
+    import shutil
+    src = os.path.dirname(fp64_emu.__file__)
+    dst = tmp_path / "fp64_emu"
+    shutil.copytree(src, dst, ignore=shutil.ignore_patterns("*.so", "__pycache__"))
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "try:\n    import fp64_emu\nexcept ImportError as e:\n"
+            "    print('IMPORT_ERROR', e); sys.exit(0)\n"
+            "sys.exit(3)\n" % str(tmp_path))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "not built" in r.stdout
