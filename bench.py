@@ -2,17 +2,19 @@
 the default plan, on one MI355X.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--n 8192] [--no-accuracy]
-                [--no-cpu]
+                [--no-cpu] [--calibrate-copy]
 
-One step = one fp64_emu.mm_nt(A, Bt) call on resident 8192x8192 float64
-operands (iid N(0,1) from CPU seeds 2000/2001, configs[1]).  W untimed
-warm-up calls, then exactly K calls between two device synchronisations;
-value = 2 n^3 / (mean ms per call).  Prints one JSON line.  Besides the
-contract fields it reports: the per-phase ms of mm_timed, native rocBLAS
+One step = one emulated mm_nt of resident 8192x8192 float64 operands (iid
+N(0,1) from CPU seeds 2000/2001, configs[1]) through the C ABI
+(fp64emu_mm_nt_events, workspace allocated once).  W untimed warm-up calls,
+then exactly K calls between two device synchronisations; value = 2 n^3 /
+(mean ms per call).  Prints one JSON line.  Besides the contract fields it
+reports: the per-phase ms (events recorded by each timed call at its phase
+boundaries), the same step through the torch op fp64_emu.mm_nt, native rocBLAS
 DGEMM (torch.matmul float64 on the device) throughput, correct bits of both
 against a device double-double GEMM, the plan-adjusted INT8 roofline
 fraction, the `roofline` object for the dominant kernel (the modular GEMM,
-duration from HIP events bracketing its launch on its stream) and the CPU
+its duration from the events bracketing its launch in every timed call) and the CPU
 baseline (the oracle port on a bounded sample of the same workload).
 """
 import argparse
@@ -38,7 +40,22 @@ def parse():
     ap.add_argument("--n", type=int, default=8192)
     ap.add_argument("--no-accuracy", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a float64 streaming kernel over 1 GiB (read 1 GiB, write "
+                         "1 GiB) three times: the scale of the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
+
+
+def calibrate_copy():
+    import torch
+    n = (1 << 30) // 8
+    src = torch.ones(n, dtype=torch.float64, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy": "torch.neg float64", "bytes_read": n * 8,
+                      "bytes_written": n * 8, "launches": 3}), flush=True)
 
 
 def log(msg):
@@ -52,6 +69,10 @@ def main():
         print("bench.py: this build runs on one GPU only (the emulated GEMM has no "
               "multi-GPU path); use --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
 
     import torch
     import fp64_emu
@@ -71,30 +92,46 @@ def main():
     torch.cuda.synchronize()
     log(f"inputs resident: {n}^3, plan P={P} corr={corr} G={G}")
 
-    for _ in range(args.warmup):
-        C = fp64_emu.mm_nt(A, Bt)
+    # Timed region: K calls through the C ABI's instrumented mm_nt on a
+    # workspace and output allocated once; every call records its phase
+    # boundaries on the stream the kernels run on (no synchronisation).
+    primes = fp64_emu._PRIMES[:P]
+    lay = capi.layout(1, M, N, K, P, corr)
+    ws = torch.empty(int(lay.total), dtype=torch.uint8, device=dev)
+    C = torch.empty(M, N, dtype=torch.float64, device=dev)
+    evs = [capi.PhaseEvents() for _ in range(max(args.steps, 1))]
+    for i in range(args.warmup):
+        capi.mm_nt_events(A, Bt, primes, C, ws, evs[i % len(evs)], use_corr=corr)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        C = fp64_emu.mm_nt(A, Bt)
+    for i in range(args.steps):
+        capi.mm_nt_events(A, Bt, primes, C, ws, evs[i], use_corr=corr)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms = elapsed * 1e3 / max(args.steps, 1)
     value = flop / (ms * 1e-3) / 1e12
     log(f"timed {args.steps} steps: {ms:.3f} ms/step, {value:.1f} TFLOP/s")
-
-    # Phases and the modular GEMM kernel's duration: mm_timed's events e1/e2
-    # bracket exactly the one modgemm launch, on its stream.
-    B = Bt.t().contiguous()
-    phases = []
-    for _ in range(max(3, args.steps)):
-        _, ph = fp64_emu.mm_timed(A, B)
-        phases.append(ph)
+    phases = [e.phases_ms() for e in evs[:max(args.steps, 1)]]
     avg = [sum(p[i] for p in phases) / len(phases) for i in range(4)]
-    gemm_ms = avg[1]
+    gemm_ms = avg[1]    # events 1 -> 2 bracket exactly the one modgemm launch
     gemm_tops = 2.0 * M * N * K * G / (gemm_ms * 1e-3) / 1e12
-    del B
     log(f"phases ms (avg of {len(phases)}): {['%.3f' % x for x in avg]}")
+    del ws, evs
+
+    # The same step through the drop-in torch op (workspace from torch's
+    # caching allocator), for comparison.
+    for _ in range(2):
+        C2 = fp64_emu.mm_nt(A, Bt)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    op_steps = max(3, min(args.steps, 10))
+    for _ in range(op_steps):
+        C2 = fp64_emu.mm_nt(A, Bt)
+    torch.cuda.synchronize()
+    op_ms = (time.perf_counter() - t0) * 1e3 / op_steps
+    assert torch.equal(C, C2), "torch op and C ABI results differ"
+    del C2
+    log(f"torch op mm_nt: {op_ms:.3f} ms/step")
 
     # Native DGEMM comparator (rocBLAS through torch.matmul float64).
     for _ in range(2):
@@ -158,6 +195,7 @@ def main():
                      "work": "2*M*N*K*G INT8 ops per launch"},
         "plan_roofline_frac": round(value / (INT8_PEAK_TOPS / G), 4),
         "phases_ms": [round(x, 4) for x in avg],
+        "torch_op_ms_per_step": round(op_ms, 4),
         "native_dgemm_tflops": round(nat_tf, 2),
         "native_dgemm_ms": round(nat_ms, 3),
         "speedup_vs_native": round(value / nat_tf, 3),

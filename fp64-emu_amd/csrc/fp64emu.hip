@@ -862,11 +862,9 @@ reconstruct_kernel(ReconArgs a) {
   for (int e = 0; e < 4; ++e) {
     const int64_t i = i0 + e;
     if (i >= a.M) continue;
-    // A group with fewer than 3 digits never reached its int64 steps.
-    long long gv[3];
-#pragma unroll
-    for (int g = 0; g < 3; ++g) gv[g] = (P > 7 * g + 2) ? ag[e][g] : (long long)h32[e][g];
-    const long long a0 = gv[0], a1 = gv[1], a2 = gv[2];
+    // Every group ends on its position-0 digit, an int64 step, so ag holds
+    // the group value whatever the group's digit count.
+    const long long a0 = ag[e][0], a1 = ag[e][1], a2 = ag[e][2];
     const int sh = -((int)a.sftA[b * a.M + i] + sj);
     double val;
     if (kExact) {
@@ -884,6 +882,12 @@ reconstruct_kernel(ReconArgs a) {
     }
     a.out[(b * a.M + i) * a.N + j] = ldexp(val, sh);
   }
+}
+
+__global__ void __launch_bounds__(kThreads) fill_zero_kernel(double* out, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads)
+    out[i] = 0.0;
 }
 
 // ---------------------------------------------------------------------------
@@ -987,7 +991,19 @@ int run(const Call& c) {
         if (int st = check_hip(hipEventRecord(c.ev[e], s), "hipEventRecord")) return st;
     return FP64EMU_OK;
   }
-  if (!c.out || !c.A || !c.B) return fail(FP64EMU_EINVAL, "null operand pointer");
+  if (!c.out) return fail(FP64EMU_EINVAL, "null operand pointer");
+  if (c.K == 0) {
+    // Empty sums: zeros, written by a kernel (no memset node under capture).
+    const int64_t n = MF * c.N;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)std::min<int64_t>((n + kThreads - 1) / kThreads, 65535)),
+                       dim3(kThreads), 0, s, c.out, n);
+    if (int st = check_hip(hipGetLastError(), "kernel launch")) return st;
+    if (c.ev)
+      for (int e = 1; e < 5; ++e)
+        if (int st = check_hip(hipEventRecord(c.ev[e], s), "hipEventRecord")) return st;
+    return FP64EMU_OK;
+  }
+  if (!c.A || !c.B) return fail(FP64EMU_EINVAL, "null operand pointer");
   if (!c.ws || c.ws_bytes < L.total) return fail(FP64EMU_EWORKSPACE, "workspace too small");
   const ModTables tab = make_tables(c.primes, c.P);
 
@@ -1202,6 +1218,25 @@ int fp64emu_mm_timed(double* out, float* times, const double* A, const double* B
   }
   for (int i = 0; i < created; ++i) (void)hipEventDestroy(ev[i]);
   return st;
+}
+
+int fp64emu_mm_nt_events(double* out, const double* A, const double* Bt, int64_t M, int64_t N,
+                         int64_t K, const int32_t* primes, const int32_t* inv, const int64_t* mu,
+                         int nprimes, int exact, int64_t bits, int use_corr, void* workspace,
+                         size_t workspace_bytes, fp64emu_stream_t stream,
+                         const fp64emu_event_t* events) {
+  (void)inv; (void)mu;
+  g_err.clear();
+  if (!events) return fail(FP64EMU_EINVAL, "events must not be NULL");
+  hipEvent_t ev[5];
+  for (int i = 0; i < 5; ++i) {
+    if (!events[i]) return fail(FP64EMU_EINVAL, "events must not be NULL");
+    ev[i] = reinterpret_cast<hipEvent_t>(events[i]);
+  }
+  Call c = make_call(out, A, Bt, 1, M, N, K, true, primes, nprimes, exact, bits, use_corr,
+                     workspace, workspace_bytes, stream);
+  c.ev = ev;
+  return run(c);
 }
 
 int fp64emu_ddgemm_nt(double* hi, double* lo, const double* A, const double* B, int64_t M,

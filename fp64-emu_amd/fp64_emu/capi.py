@@ -22,7 +22,7 @@ TILE_R, TILE_K, FRAG = 256, 64, 1024
 # Every function declared in include/fp64emu.h.
 EXPORTS = ("fp64emu_maxp", "fp64emu_last_error", "fp64emu_workspace_size", "fp64emu_mm",
            "fp64emu_mm_nt", "fp64emu_bmm", "fp64emu_bmm_nt", "fp64emu_mm_timed",
-           "fp64emu_layout", "fp64emu_ddgemm_nt")
+           "fp64emu_mm_nt_events", "fp64emu_layout", "fp64emu_ddgemm_nt")
 
 
 class Layout(ctypes.Structure):
@@ -64,6 +64,8 @@ def lib():
     L.fp64emu_mm_timed.argtypes = [vp, vp, vp, vp, i64, i64, i64, vp, vp, vp, i32, i32, i64, i32,
                                    vp, sz, vp]
     L.fp64emu_mm_timed.restype = i32
+    L.fp64emu_mm_nt_events.argtypes = mm_args + [ctypes.POINTER(ctypes.c_void_p)]
+    L.fp64emu_mm_nt_events.restype = i32
     L.fp64emu_layout.argtypes = [i64, i64, i64, i64, i32, i32, ctypes.POINTER(Layout)]
     L.fp64emu_layout.restype = i32
     L.fp64emu_ddgemm_nt.argtypes = [vp, vp, vp, vp, i64, i64, i64, vp]
@@ -139,6 +141,34 @@ def mm_timed(A, B, primes, exact=True, bits=53, use_corr=True):
                                   primes.size, int(bool(exact)), int(bits),
                                   int(bool(use_corr)), ws.data_ptr(), ws.numel(), _stream()))
     return out, list(times)
+
+
+class PhaseEvents:
+    """Five timing events for fp64emu_mm_nt_events, created through torch
+    on the current stream (recorded once so their HIP handles exist)."""
+
+    def __init__(self):
+        self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+        for e in self.ev:
+            e.record()
+        self.handles = (ctypes.c_void_p * 5)(*[e.cuda_event for e in self.ev])
+
+    def phases_ms(self):
+        """[sizing+extract, gemms, 0-marker, reconstruct] after a sync."""
+        return [self.ev[i].elapsed_time(self.ev[i + 1]) for i in range(4)]
+
+
+def mm_nt_events(A, Bt, primes, out, ws, events, exact=True, bits=53, use_corr=True):
+    """fp64emu_mm_nt_events on preallocated `out` and workspace `ws`."""
+    primes = np.ascontiguousarray(np.asarray(primes, dtype=np.int32))
+    M, K = A.shape
+    N = Bt.shape[1]
+    _check(lib().fp64emu_mm_nt_events(out.data_ptr(), A.data_ptr(), Bt.data_ptr(), M, N, K,
+                                      primes.ctypes.data_as(ctypes.c_void_p), None, None,
+                                      primes.size, int(bool(exact)), int(bits),
+                                      int(bool(use_corr)), ws.data_ptr(), ws.numel(), _stream(),
+                                      events.handles))
+    return out
 
 
 def ddgemm_nt(A, B):

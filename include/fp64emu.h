@@ -39,8 +39,9 @@
 extern "C" {
 #endif
 
-/* hipStream_t, kept opaque so this header needs no HIP include. */
+/* hipStream_t / hipEvent_t, kept opaque so this header needs no HIP include. */
 typedef struct ihipStream_t* fp64emu_stream_t;
+typedef struct ihipEvent_t* fp64emu_event_t;
 
 #define FP64EMU_MAXP 20
 
@@ -96,6 +97,17 @@ int fp64emu_mm_timed(double* out, float* times /* host, 4 floats */, const doubl
                      const int32_t* inv, const int64_t* mu, int nprimes, int exact, int64_t bits,
                      int use_corr, void* workspace, size_t workspace_bytes,
                      fp64emu_stream_t stream);
+
+/* fp64emu_mm_nt that also records five caller-created events on `stream`
+ * at the phase boundaries [start, extracted, gemms done, gemms done,
+ * reconstructed] (the boundaries of fp64emu_mm_timed) and does not
+ * synchronize.  No reference counterpart: it lets a benchmark time each
+ * kernel inside its timed loop, on the stream the kernels run on. */
+int fp64emu_mm_nt_events(double* out, const double* A, const double* Bt, int64_t M, int64_t N,
+                         int64_t K, const int32_t* primes, const int32_t* inv, const int64_t* mu,
+                         int nprimes, int exact, int64_t bits, int use_corr, void* workspace,
+                         size_t workspace_bytes, fp64emu_stream_t stream,
+                         const fp64emu_event_t* events /* host, 5 events */);
 
 /* ---- Workspace map (inspection of intermediates; no reference
  * counterpart: the reference's scratch is private torch tensors).  After a

@@ -113,3 +113,37 @@ def check_call(kind, A, B, primes, exact=True, bits=53, use_corr=True, full_orac
         assert info["bits_eff"] == gbe
         assert bits_equal(outh, oout), "whole pipeline differs from the oracle"
     return out, ws, lay
+
+
+def sampled_parity(kind, A, B, primes, rows, cols, exact=True, bits=53, use_corr=True):
+    """Parity at sizes the oracle cannot finish whole: run the C-ABI call,
+    then check (1) the sizing (shifts, width) against the oracle's sizing of
+    the full operands, and (2) the outputs at rows x cols bit-exact against
+    the oracle's extraction, modular GEMMs and reconstruction of just those
+    rows and columns at that sizing.  2-D kinds only.  Returns
+    (out, bits_eff, workspace layout, device workspace)."""
+    b_kn = kind == "mm_nt"
+    out, ws, lay = capi.run(kind, A, B, primes, exact=exact, bits=bits, use_corr=use_corr)
+    torch.cuda.synchronize()
+    primes = np.asarray(primes, dtype=np.int32)
+    head = ws[:lay.off_planesA].cpu().numpy()
+    gsA, gsB, _, _, gbe = capi.sizing(head, lay)
+    Ah, Bh = A.cpu().numpy(), B.cpu().numpy()
+    obe, osA, osB, _, _ = oracle_sizing(Ah, Bh, b_kn, primes, bits)
+    assert gbe == obe, f"bits_eff GPU {gbe} oracle {obe}"
+    assert np.array_equal(gsA, osA) and np.array_equal(gsB, osB), "shifts differ"
+
+    rows = np.asarray(sorted(set(int(r) for r in rows)))
+    cols = np.asarray(sorted(set(int(c) for c in cols)))
+    As = np.ascontiguousarray(Ah[rows])[None]
+    Bs = np.ascontiguousarray(Bh[:, cols] if b_kn else Bh[cols])[None]
+    rA, hA, qA = O.extract_operand(As, 0, gsA[rows], gbe, primes, use_corr)
+    rB, hB, qB = O.extract_operand(Bs, 1 if b_kn else 0, gsB[cols], gbe, primes, use_corr)
+    res = np.stack([O.modgemm(rA[0, t], rB[0, t], int(primes[t])) for t in range(primes.size)])
+    c1 = O.modgemm(hA[0], qB[0], 0) if use_corr else None
+    c2 = O.modgemm(qA[0], hB[0], 0) if use_corr else None
+    rec = O.reconstruct(res, c1, c2, primes, gbe, gsA[rows], gsB[cols], exact)
+    got = out.cpu().numpy()[np.ix_(rows, cols)]
+    assert bits_equal(got, rec), "sampled outputs differ from the oracle"
+    del Ah, Bh
+    return out, gbe, lay, ws

@@ -1,0 +1,298 @@
+"""GPU tier: the reference's own test suite (tests/test_fp64_emu.py),
+re-expressed with CPU-seeded inputs, through the drop-in Python API and torch
+ops; plus graph capture, streams, mm_timed, error messages and empty shapes.
+
+Where the reference asserts a statistical floor (>= 45 bits against torch's
+float64 matmul) the same floor is kept and, where the inputs make the product
+exactly representable, the exact result is asserted as well.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import fp64_emu as emu
+import oracle as O
+from fp64_emu import capi
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _randn(shape, seed, dev):
+    return torch.randn(shape, dtype=torch.float64, generator=_gen(seed)).to(dev)
+
+
+def _randint(lo, hi, shape, seed, dev):
+    return torch.randint(lo, hi, shape, generator=_gen(seed), dtype=torch.int64).double().to(dev)
+
+
+def _bits_vs(C, ref):
+    rel = (C - ref).abs().max().item() / ref.abs().max().item()
+    return -math.log2(rel) if rel > 0 else 53.0
+
+
+def _dd_bits(C, A, Bt):
+    hi, lo = capi.ddgemm_nt(A, Bt.t().contiguous())
+    torch.cuda.synchronize()
+    return O.correct_bits(C.cpu().numpy(), hi.cpu().numpy(), lo.cpu().numpy())
+
+
+def test_integer_products_accurate(dev):
+    """test_fp64_emu.py:14-25: integers in [-1000, 1000], nprimes=18."""
+    print("case integer_products_accurate", flush=True)
+    A = _randint(-1000, 1001, (128, 256), 0, dev)
+    Bt = _randint(-1000, 1001, (256, 96), 1, dev)
+    ref = torch.from_numpy(A.cpu().numpy().astype(np.int64) @ Bt.cpu().numpy().astype(np.int64))
+    C = emu.mm_nt(A, Bt, nprimes=18)
+    assert _bits_vs(C, ref.double().to(dev)) >= 45.0
+    assert torch.equal(C.cpu(), ref.double())
+
+
+def test_exact_mode_bitwise_integer_oracle(dev):
+    """test_fp64_emu.py:28-39: integers in [-4096, 4096], nprimes=20, exact."""
+    print("case exact_mode_bitwise_integer_oracle", flush=True)
+    A = _randint(-4096, 4097, (128, 256), 2, dev)
+    Bt = _randint(-4096, 4097, (256, 96), 3, dev)
+    ref = (A.cpu().long() @ Bt.cpu().long()).double()
+    assert torch.equal(emu.mm_nt(A, Bt, nprimes=20, exact=True).cpu(), ref)
+
+
+@pytest.mark.parametrize("nprimes", [18, 20])
+def test_random_fp64_accuracy(dev, nprimes):
+    """test_fp64_emu.py:42-50, plus correct bits against the double-double
+    reference at least native float64's."""
+    print(f"case random_fp64_accuracy nprimes={nprimes}", flush=True)
+    A = _randn((512, 1024), 4, dev)
+    Bt = _randn((1024, 512), 5, dev)
+    native = A @ Bt
+    C = emu.mm_nt(A, Bt, nprimes=nprimes)
+    assert _bits_vs(C, native) >= 45.0
+    assert _dd_bits(C, A, Bt) >= _dd_bits(native, A, Bt)
+
+
+def test_range_rule_adversarial_aligned(dev):
+    """test_fp64_emu.py:53-63: all-ones, K=2048, every dot product K 2^104
+    in the scaled domain, exact at the default plan."""
+    print("case range_rule_adversarial_aligned", flush=True)
+    K = 2048
+    A = torch.ones(64, K, dtype=torch.float64, device=dev)
+    Bt = torch.ones(K, 48, dtype=torch.float64, device=dev)
+    C = emu.mm_nt(A, Bt, exact=True)
+    assert torch.equal(C, torch.full((64, 48), float(K), dtype=torch.float64, device=dev))
+
+
+def test_dyadic_dynamic_range_bitexact(dev):
+    """test_fp64_emu.py:66-83: integers under per-k power-of-two scales
+    2^-12..2^0; exact at defaults through mm."""
+    print("case dyadic_dynamic_range_bitexact", flush=True)
+    g = _gen(6)
+    M, K, N = 64, 512, 48
+    ek = torch.randint(-12, 1, (K,), generator=g)
+    Ai = torch.randint(-256, 257, (M, K), generator=g)
+    Bi = torch.randint(-256, 257, (N, K), generator=g)
+    A = (torch.bitwise_left_shift(Ai, ek + 12).double() * 2.0 ** -12).to(dev)
+    B = (torch.bitwise_left_shift(Bi, ek + 12).double() * 2.0 ** -12).to(dev)
+    w = 4 ** (ek + 12)
+    ref = ((Ai * w) @ Bi.T).double() * 2.0 ** -24
+    assert torch.equal(emu.mm(A, B).cpu(), ref)
+
+
+def test_bmm_single_batch_matches_mm(dev):
+    """test_fp64_emu.py:86-94."""
+    print("case bmm_single_batch_matches_mm", flush=True)
+    A = _randn((192, 384), 7, dev)
+    B = _randn((160, 384), 8, dev)
+    assert torch.equal(emu.bmm(A[None], B[None])[0], emu.mm(A, B))
+
+
+def test_bmm_integer_oracle_bitexact(dev):
+    """test_fp64_emu.py:97-104."""
+    print("case bmm_integer_oracle_bitexact", flush=True)
+    A = _randint(-4096, 4097, (5, 96, 256), 9, dev)
+    B = _randint(-4096, 4097, (5, 64, 256), 10, dev)
+    ref = torch.stack([(A[b].cpu().long() @ B[b].cpu().long().T).double() for b in range(5)])
+    assert torch.equal(emu.bmm(A, B).cpu(), ref)
+
+
+def test_bmm_odd_shapes_accuracy(dev):
+    """test_fp64_emu.py:107-119."""
+    print("case bmm_odd_shapes_accuracy", flush=True)
+    A = _randn((3, 100, 333), 11, dev)
+    Bt = _randn((3, 333, 77), 12, dev)
+    ref = torch.bmm(A, Bt)
+    C = emu.bmm_nt(A, Bt)
+    assert _bits_vs(C, ref) >= 45.0
+
+
+def test_mm_nt_and_mm_layouts_agree(dev):
+    """test_fp64_emu.py:147-161 in this build's terms: the [K, N] layout read
+    in place and the [N, K] layout give identical bits (the shifts are exact
+    and the width decision agrees)."""
+    print("case mm_nt_and_mm_layouts_agree", flush=True)
+    A = _randn((256, 1024), 13, dev)
+    Bt = _randn((1024, 200), 14, dev)
+    assert torch.equal(emu.mm_nt(A, Bt), emu.mm(A, Bt.t().contiguous()))
+
+
+def test_graph_capture_replays(dev):
+    """test_fp64_emu.py:164-182, strengthened: several replays with eager work
+    and synchronisation between them; each replay equals the eager result on
+    the buffers' current contents."""
+    print("case graph_capture_replays", flush=True)
+    A = _randn((128, 256), 15, dev)
+    B = _randn((96, 256), 16, dev)
+    for _ in range(3):
+        emu.mm(A, B)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        C = emu.mm(A, B)
+    for r in range(4):
+        A.copy_(_randn((128, 256), 100 + r, dev))
+        B.copy_(_randn((96, 256), 200 + r, dev))
+        g.replay()
+        torch.cuda.synchronize()
+        eager = emu.mm(A, B)
+        torch.cuda.synchronize()
+        assert torch.equal(C, eager), f"replay {r}"
+        emu.mm_nt(A, B.t().contiguous())   # unrelated eager work between replays
+
+
+def test_torch_compile_traces(dev):
+    """test_fp64_emu.py:185-193."""
+    print("case torch_compile_traces", flush=True)
+    A = _randn((64, 128), 17, dev)
+    B = _randn((48, 128), 18, dev)
+    eager = emu.mm(A, B)
+    compiled = torch.compile(emu.mm, dynamic=False)
+    assert torch.equal(compiled(A, B), eager)
+
+
+def test_deterministic(dev):
+    """test_fp64_emu.py:196-211."""
+    print("case deterministic", flush=True)
+    A = _randn((4, 128, 512), 19, dev)
+    B = _randn((4, 96, 512), 20, dev)
+    assert torch.equal(emu.bmm(A, B), emu.bmm(A, B))
+    A = _randn((256, 512), 21, dev)
+    Bt = _randn((512, 256), 22, dev)
+    assert torch.equal(emu.mm_nt(A, Bt, nprimes=18), emu.mm_nt(A, Bt, nprimes=18))
+
+
+def test_side_stream(dev):
+    """Work is enqueued on the caller's current stream."""
+    print("case side_stream", flush=True)
+    A = _randn((300, 700), 23, dev)
+    Bt = _randn((700, 200), 24, dev)
+    ref = emu.mm_nt(A, Bt)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        C = emu.mm_nt(A, Bt)
+    s.synchronize()
+    assert torch.equal(C, ref)
+
+
+def test_mm_timed_contract(dev):
+    """torch-ext/fp64_emu/__init__.py:135-149: (C, [extract, gemms, 0, reconstruct])."""
+    print("case mm_timed_contract", flush=True)
+    A = _randn((512, 2048), 25, dev)
+    B = _randn((384, 2048), 26, dev)
+    C, t = emu.mm_timed(A, B)
+    assert isinstance(t, list) and len(t) == 4
+    # t[2] spans two back-to-back events (the reference's 0-marker)
+    assert t[0] > 0 and t[1] > 0 and t[3] > 0 and 0.0 <= t[2] < t[1]
+    assert torch.equal(C, emu.mm(A, B))
+
+
+def test_op_error_messages(dev):
+    """The reference's TORCH_CHECK messages (fp64_emu_cuda/fp64_emu.cu:1586-1693)
+    surface as RuntimeError."""
+    print("case op_error_messages", flush=True)
+    ops = torch.ops.fp64_emu
+    primes, inv, mu = emu._tables(14)
+    A = _randn((8, 16), 27, dev)
+    Bt = _randn((16, 8), 28, dev)
+    out = torch.empty(8, 8, dtype=torch.float64, device=dev)
+    with pytest.raises(RuntimeError, match=r"bits must be in \[16, 53\]"):
+        ops.fp64_emu_mm_nt(out, A, Bt, primes, inv, mu, True, 15, True)
+    with pytest.raises(RuntimeError, match="f64"):
+        ops.fp64_emu_mm_nt(out, A.float(), Bt, primes, inv, mu, True, 53, True)
+    with pytest.raises(RuntimeError, match="contig"):
+        ops.fp64_emu_mm_nt(out, A.t(), Bt, primes, inv, mu, True, 53, True)
+    with pytest.raises(RuntimeError):
+        ops.fp64_emu_mm_nt(out, A, Bt[:8], primes, inv, mu, True, 53, True)
+    bad = torch.tensor(list(range(2, 24)), dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="too many primes"):
+        ops.fp64_emu_mm_nt(out, A, Bt, bad, inv, mu, True, 53, True)
+    with pytest.raises(AssertionError):
+        emu.mm_nt(A, Bt.t().contiguous())   # Python dim checks are asserts
+
+
+def test_empty_and_degenerate_shapes(dev):
+    print("case empty_and_degenerate_shapes", flush=True)
+    A = _randn((0, 16), 29, dev)
+    Bt = _randn((16, 8), 30, dev)
+    assert emu.mm_nt(A, Bt).shape == (0, 8)
+    A = torch.empty(5, 0, dtype=torch.float64, device=dev)
+    Bt = torch.empty(0, 7, dtype=torch.float64, device=dev)
+    C = emu.mm_nt(A, Bt)
+    assert C.shape == (5, 7) and not C.any()
+    A = torch.zeros(33, 40, dtype=torch.float64, device=dev)
+    A[3] = _randn((40,), 31, dev)
+    B = _randn((9, 40), 32, dev)
+    C = emu.mm(A, B)
+    assert not C[:3].any() and not C[4:].any()
+    assert _bits_vs(C[3], A[3] @ B.t()) >= 50.0
+    one = emu.mm(_randn((1, 1), 33, dev), _randn((1, 1), 34, dev))
+    assert one.shape == (1, 1)
+
+
+def test_inexact_recombine_accuracy(dev):
+    """exact=False (the fp64 combine): correct bits within a bit of exact."""
+    print("case inexact_recombine_accuracy", flush=True)
+    A = _randn((256, 2048), 35, dev)
+    Bt = _randn((2048, 256), 36, dev)
+    ce = emu.mm_nt(A, Bt, exact=True)
+    ci = emu.mm_nt(A, Bt, exact=False)
+    assert _dd_bits(ci, A, Bt) >= _dd_bits(ce, A, Bt) - 1.0
+
+
+@pytest.mark.parametrize("bits", [53, 50, 44, 40, 36, 32])
+def test_bits_sweep(dev, bits):
+    """bench/accuracy.py:143-151: each width at plan(K, bits) reaches about
+    its width in correct bits."""
+    print(f"case bits_sweep bits={bits}", flush=True)
+    A = _randn((256, 1024), 37, dev)
+    Bt = _randn((1024, 256), 38, dev)
+    C = emu.mm_nt(A, Bt, nprimes=emu.plan(1024, bits), bits=bits)
+    assert _dd_bits(C, A, Bt) >= bits - 6
+
+
+def test_beats_native_fp64(dev):
+    """test_fp64_emu.py:214-226 at the headline size: on MI355X (78.6 TF
+    FP64 matrix) the target is to beat native DGEMM at n=8192; the
+    reference's 3x factor is for GPUs with a 1/64-rate FP64 unit."""
+    import time
+    print("case beats_native_fp64 n=8192", flush=True)
+    n = 8192
+    A = _randn((n, n), 39, dev)
+    Bt = _randn((n, n), 40, dev)
+
+    def t(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / 4
+
+    assert t(lambda: A @ Bt) / t(lambda: emu.mm_nt(A, Bt)) > 1.0

@@ -66,3 +66,18 @@ def test_wide_range_parity(dev):
         e = torch.randint(-20, 21, shape, generator=g)
         return (s * m * torch.pow(2.0, e.double())).to(dev)
     check_call("mm_nt", wide((200, 700)), wide((700, 150)), O.PRIMES[:14])
+
+
+@pytest.mark.parametrize("P", list(range(1, 21)))
+def test_full_range_every_modulus_count(dev, P):
+    """Aligned operands (entries 1 + small noise, rows of either sign) make
+    the Cauchy-Schwarz bound nearly tight, so the products reach the top of
+    the CRT range and the highest Garner digit is nonzero: every group split
+    of the reconstruction (1..20 moduli) against the oracle."""
+    print(f"case full-range mm_nt 96x80x512 P={P}", flush=True)
+    g = torch.Generator().manual_seed(700 + P)
+    A = 1 + 0.01 * torch.randn((96, 512), dtype=torch.float64, generator=g)
+    A[::3] *= -1
+    B = 1 + 0.01 * torch.randn((512, 80), dtype=torch.float64, generator=g)
+    B[:, ::5] *= -1
+    check_call("mm_nt", A.to(dev), B.to(dev), O.PRIMES[:P], use_corr=P >= 12)
