@@ -207,9 +207,9 @@ def main():
 
 def cpu_baseline(A, Bt, P, corr):
     """The oracle port (the reference pipeline restated in C) on the host's
-    cores, on a bounded sample of the workload: the first 1024 rows of A and
-    columns of Bt at the full depth K, same plan.  Effective FP64 TFLOPS of
-    that sample (2 * 1024 * 1024 * K / t)."""
+    cores, on a bounded sample of the workload: the first 2048 rows of A and
+    columns of Bt at the full depth K, same plan (about 10 s on 16 cores).
+    Effective FP64 TFLOPS of that sample (2 * 2048 * 2048 * K / t)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     try:
@@ -218,7 +218,7 @@ def cpu_baseline(A, Bt, P, corr):
     except Exception:
         cores = os.cpu_count() or 1
     cores = max(1, min(cores, 16))
-    m = 1024
+    m = 2048
     a = A[:m].cpu().numpy()
     bt = Bt[:, :m].contiguous().cpu().numpy()
     K = a.shape[1]
