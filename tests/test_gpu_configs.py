@@ -8,6 +8,8 @@ inputs generated on the CPU from fixed seeds (1000*cfg, 1000*cfg + 1):
   those rows and columns;
 - correct bits against the device double-double GEMM at least native
   float64's (torch matmul on the same GPU);
+- the effective width within one bit of the values computed independently
+  from the distributions (c2 49, c3a 50, c3b 49, c5 51, c5 reduced 43);
 - c3b: the integer product bit for bit, with both correction products zero;
 - c4: every stage of all 64 members against the oracle.
 """
@@ -77,6 +79,7 @@ def test_c3a_wide_range_4096(dev):
     Bt = _wide((n, n), _gen(3001)).to(dev)
     out, be, _, ws = sampled_parity("mm_nt", A, Bt, O.PRIMES[:14], _rows(n, 3), _rows(n, 4))
     del ws
+    assert abs(be - 50) <= 1
     emu_bits, nat_bits = _native_and_emu_bits(out, A, Bt)
     print(f"c3a bits_eff {be} correct bits emu {emu_bits:.2f} native {nat_bits:.2f}", flush=True)
     assert emu_bits >= nat_bits
@@ -91,6 +94,7 @@ def test_c3b_integer_exact_4096(dev):
     A = torch.randint(-2 ** 20, 2 ** 20 + 1, (n, n), generator=_gen(3100)).double().to(dev)
     Bt = torch.randint(-2 ** 20, 2 ** 20 + 1, (n, n), generator=_gen(3101)).double().to(dev)
     out, be, lay, ws = sampled_parity("mm_nt", A, Bt, O.PRIMES[:14], _rows(n, 5), _rows(n, 6))
+    assert abs(be - 49) <= 1
     assert torch.equal(out, A @ Bt)
     rows = _rows(n, 7, 8)
     exact = A.cpu().numpy()[rows].astype(np.int64) @ Bt.cpu().numpy().astype(np.int64)
@@ -122,9 +126,11 @@ def test_c5_ragged_deep_k(dev, P, corr):
     Bt = (torch.rand((K, N), dtype=torch.float64, generator=_gen(5001)) * 2 - 1).to(dev)
     if corr:
         assert emu.plan_config(K) == (P, corr)
+    expect_be = 51 if corr else 43
     out, be, lay, ws = sampled_parity("mm_nt", A, Bt, O.PRIMES[:P], _rows(M, 8), _rows(N, 9),
                                       use_corr=corr)
     del ws
+    assert abs(be - expect_be) <= 1
     assert torch.equal(out, emu.mm_nt(A, Bt, nprimes=P, corr=corr))
     emu_bits, nat_bits = _native_and_emu_bits(out, A, Bt)
     print(f"c5 P={P} bits_eff {be} correct bits emu {emu_bits:.2f} native {nat_bits:.2f}",
