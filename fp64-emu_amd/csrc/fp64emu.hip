@@ -46,6 +46,8 @@ constexpr int kOutBlkBytes = 256;                // one 16x16 int8 output block
 constexpr int kMaxSlab = 128;
 constexpr int64_t kMaxKSingle = 131071;          // int32 accumulator bound: K * 128^2 < 2^31
 constexpr int64_t kMaxKFusedCorr = 65536;        // 2K * 127^2 < 2^31: both cross GEMMs in one
+constexpr int64_t kSegK = 65536;                 // K-segmented path: segment depth
+constexpr int64_t kMaxKDeep = 128 * kSegK;       // the reference's segmented bound
 // x + kMagic (|x| < 2^51) lands on the integer grid of [2^52, 2^53): the sum
 // rounds x to the nearest integer, ties to even.
 constexpr double kMagic = 6755399441055744.0;
@@ -140,13 +142,19 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   std::memset(L, 0, sizeof(*L));
   L->batch = batch; L->M = M; L->N = N; L->K = K;
   L->nprimes = P; L->use_corr = corr ? 1 : 0;
-  L->ncorr = corr ? (K <= kMaxKFusedCorr ? 1 : 2) : 0;
+  // K-segmented (K > 131071, B as [N, K]): planes hold one segment; each
+  // segment's correction is one fused GEMM; the GEMMs accumulate into int32
+  // residue sums and one int64 correction sum.
+  L->deep = K > kMaxKSingle ? 1 : 0;
+  L->kseg = L->deep ? kSegK : K;
+  L->nseg = L->deep ? (int)((K + kSegK - 1) / kSegK) : 1;
+  L->ncorr = corr ? ((L->deep || K <= kMaxKFusedCorr) ? 1 : 2) : 0;
   int64_t kslab; int nslab;
   slab_split(batch * N, K, &kslab, &nslab);
   L->nslab = nslab;
   L->Mp = round_up(std::max<int64_t>(M, 1), kTileR);
   L->Np = round_up(std::max<int64_t>(N, 1), kTileR);
-  L->Kp = round_up(K, kTileK);
+  L->Kp = round_up(L->kseg, kTileK);
   L->planeA_bytes = L->Mp * L->Kp;
   L->planeB_bytes = L->Np * L->Kp;
   const int nplanes = P + (corr ? 2 : 0);   // the correction plane is 2*Kp deep
@@ -164,8 +172,9 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   L->off_pss = take(sizeof(double) * (size_t)nslab * batch * N);
   L->off_planesA = take((size_t)(batch * L->memberA_bytes));
   L->off_planesB = take((size_t)(batch * L->memberB_bytes));
-  L->off_res8 = take((size_t)(batch * P * L->outplane_bytes));
-  L->off_corr = take(sizeof(int32_t) * (size_t)(batch * L->ncorr * L->outplane_bytes));
+  L->off_res8 = take((L->deep ? sizeof(int32_t) : 1) * (size_t)(batch * P * L->outplane_bytes));
+  L->off_corr = take((L->deep ? sizeof(int64_t) : sizeof(int32_t)) *
+                     (size_t)(batch * L->ncorr * L->outplane_bytes));
   L->total = o;
 }
 
@@ -328,7 +337,8 @@ __device__ __forceinline__ uint64_t rne_shift_right(uint64_t mag, int s) {
 struct ExtractArgs {
   const double* A;
   const double* B;
-  int64_t M, N, K, batch;
+  int64_t M, N, K, batch;   // K: depth extracted by this launch (one segment)
+  int64_t lda, k0;          // full operand depth and this segment's first k
   int b_kn;          // B given as [K, N] (mm_nt / bmm_nt)
   int use_corr;
   int64_t nkt;       // Kp / 64
@@ -385,11 +395,11 @@ extract_kernel(ExtractArgs a) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) x[j] = 0.0;
   } else if (kn) {
-    const double* __restrict__ src = a.B + (b * K + k0) * a.N + r;
+    const double* __restrict__ src = a.B + (b * a.lda + a.k0 + k0) * a.N + r;
 #pragma unroll
     for (int j = 0; j < 16; ++j) x[j] = (k0 + j < K) ? src[(int64_t)j * a.N] : 0.0;
   } else {
-    const double* __restrict__ src = (isA ? a.A : a.B) + (b * R + r) * K + k0;
+    const double* __restrict__ src = (isA ? a.A : a.B) + (b * R + r) * a.lda + a.k0 + k0;
     if (k0 + 16 <= K) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) x[j] = src[j];
@@ -492,6 +502,9 @@ struct GemmArgs {
   const int8_t* B;
   int8_t* res8;
   int32_t* corr;
+  int32_t* racc;       // K-segmented: residue sums (instead of res8)
+  int64_t* cacc;       // K-segmented: correction sum (instead of corr)
+  int first;           // K-segmented: first segment stores, later ones add
   int64_t memberA, memberB, planeA, planeB;
   int64_t outplane;    // Mp * Np
   int64_t total;       // work groups
@@ -525,10 +538,21 @@ __device__ __forceinline__ void barrier_lds() {
 
 typedef __attribute__((address_space(3))) int8_t lds_i8;
 
+// One accumulator element read at its point of use.  With plain element
+// reads the compiler copies all 256 accumulators to VGPRs at the loop exit,
+// which overflows the VGPR file and spills; an AGPR operand keeps each value
+// in place until its own read.
+__device__ __forceinline__ int acc_read(int a) {
+  int v;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+  return v;
+}
+
 constexpr int kStages = 4;                   // LDS ring: 4 x 32 KiB
 constexpr int kStageBytes = 2 * kTileBytes;  // A tile then B tile
 constexpr int kDmaPerStep = 8;               // per wave: 4 KiB of A + 4 KiB of B
 
+template <bool kDeep>
 __global__ void __launch_bounds__(kThreads, 1)
 modgemm_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) int8_t lds[kStages * kStageBytes];
@@ -656,42 +680,84 @@ modgemm_kernel(GemmArgs g) {
   // Epilogue: 32x32 blocks (mb, nb) of this wave, 16 values per lane.
   const int64_t NB = (int64_t)g.TN * 8;                 // 32-blocks per output row
   const int64_t mb0 = (int64_t)mt * 8 + wm * 4, nb0 = (int64_t)nt * 8 + wn * 4;
-  if (is_corr) {
-    int32_t* dst = g.corr + (b * g.ncorr + slot) * g.outplane;
+  if (kDeep && is_corr) {
+    // K-segmented: this segment's correction products join the int64 sum.
+    typedef long long v2l __attribute__((ext_vector_type(2)));
+    int64_t* dst = g.cacc + b * g.outplane;
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        v2l* d = reinterpret_cast<v2l*>(dst + ((mb0 + x) * NB + nb0 + y) * 1024 + lane * 16);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          v2l v = v2l{(long long)acc[x][y][2 * q], (long long)acc[x][y][2 * q + 1]};
+          if (!g.first) v += d[q];
+          d[q] = v;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+  } else if (kDeep) {
+    // K-segmented: balanced residues of this segment join the int32 sums.
+    const int t = plane;
+    const double pd = (double)g.p[t], ip = g.invp[t];
+    int32_t* dst = g.racc + (b * g.P + t) * g.outplane;
 #pragma unroll
     for (int x = 0; x < 4; ++x)
 #pragma unroll
       for (int y = 0; y < 4; ++y) {
         v4i* d = reinterpret_cast<v4i*>(dst + ((mb0 + x) * NB + nb0 + y) * 1024 + lane * 16);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          d[q] = v4i{acc[x][y][4 * q], acc[x][y][4 * q + 1], acc[x][y][4 * q + 2], acc[x][y][4 * q + 3]};
+        for (int q = 0; q < 4; ++q) {
+          v4i v;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const double av = (double)acc[x][y][4 * q + u];
+            const double qq = fma(av, ip, kMagic) - kMagic;
+            // +p/2 (p = 256) is -p/2 in the balanced range: the int8 value
+            v[u] = (int)(int8_t)(uint8_t)((uint32_t)(int)fma(-qq, pd, av) & 0xFFu);
+          }
+          if (!g.first) v += d[q];
+          d[q] = v;
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
   } else {
-    const int t = plane;
+    // One block at a time, the slot kind a uniform branch inside: both kinds
+    // keep the same live ranges (two separate loops made the compiler spill
+    // an accumulator tile at the split).
+    const int t = is_corr ? 0 : plane;
     const double pd = (double)g.p[t], ip = g.invp[t];
-    int8_t* dst = g.res8 + (b * g.P + t) * g.outplane;
+    int32_t* cdst = g.corr + (b * g.ncorr + (is_corr ? slot : 0)) * g.outplane;
+    int8_t* rdst = g.res8 + (b * g.P + t) * g.outplane;
 #pragma unroll
     for (int x = 0; x < 4; ++x)
 #pragma unroll
       for (int y = 0; y < 4; ++y) {
-        uint32_t w[4];
+        const int64_t blk = ((mb0 + x) * NB + nb0 + y) * 1024 + lane * 16;
+        if (is_corr) {
+          v4i* d = reinterpret_cast<v4i*>(cdst + blk);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          uint32_t u = 0u;
+          for (int q = 0; q < 4; ++q)
+            d[q] = v4i{acc_read(acc[x][y][4 * q]), acc_read(acc[x][y][4 * q + 1]),
+                       acc_read(acc[x][y][4 * q + 2]), acc_read(acc[x][y][4 * q + 3])};
+        } else {
+          uint32_t w[4];
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            // |acc| < 2^31: the nearest quotient is exact (see extraction).
-            const double av = (double)acc[x][y][4 * q + v];
-            const double qq = fma(av, ip, kMagic) - kMagic;
-            const int rr = (int)fma(-qq, pd, av);
-            u |= ((uint32_t)rr & 0xFFu) << (8 * v);
+          for (int q = 0; q < 4; ++q) {
+            uint32_t u = 0u;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              // |acc| < 2^31: the nearest quotient is exact (see extraction).
+              const double av = (double)acc_read(acc[x][y][4 * q + v]);
+              const double qq = fma(av, ip, kMagic) - kMagic;
+              const int rr = (int)fma(-qq, pd, av);
+              u |= ((uint32_t)rr & 0xFFu) << (8 * v);
+            }
+            w[q] = u;
           }
-          w[q] = u;
+          *reinterpret_cast<v4i*>(rdst + blk) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
         }
-        *reinterpret_cast<v4i*>(dst + ((mb0 + x) * NB + nb0 + y) * 1024 + lane * 16) =
-            v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
         __builtin_amdgcn_sched_barrier(0);
       }
   }
@@ -738,6 +804,8 @@ __device__ __forceinline__ double i128_to_f64(i128 v) {
 struct ReconArgs {
   const int8_t* res8;
   const int32_t* corr;
+  const int32_t* res32;   // K-segmented: residue sums, folded here
+  const int64_t* corr64;  // K-segmented: correction sum
   double* out;
   const int16_t* sftA;
   const int16_t* sftB;
@@ -750,7 +818,7 @@ struct ReconArgs {
   ModTables tab;
 };
 
-template <bool kExact>
+template <bool kExact, bool kDeep>
 __global__ void __launch_bounds__(kThreads)
 reconstruct_kernel(ReconArgs a) {
   const int64_t blk = blockIdx.x;
@@ -768,11 +836,34 @@ reconstruct_kernel(ReconArgs a) {
   const int P = a.tab.P;
   const int64_t boff = (mb * a.NB + nb) * 1024 + 4 * thr;  // byte (int8) / element (int32)
   uint32_t w[kMaxP];
-#pragma unroll
-  for (int t = 0; t < kMaxP; ++t)
-    if (t < P) w[t] = *reinterpret_cast<const uint32_t*>(a.res8 + (b * P + t) * a.outplane + boff);
   int64_t cv[4] = {0, 0, 0, 0};
-  if (a.ncorr > 0) {
+  if (kDeep) {
+    // Fold the segment sums (|sum| <= 128 per segment) to balanced residues.
+#pragma unroll
+    for (int t = 0; t < kMaxP; ++t)
+      if (t < P) {
+        const v4i v = *reinterpret_cast<const v4i*>(a.res32 + (b * P + t) * a.outplane + boff);
+        const double pd = (double)a.tab.p[t], ip = a.tab.invp[t];
+        uint32_t u = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const double vd = (double)v[e];
+          const double qq = fma(vd, ip, kMagic) - kMagic;
+          u |= ((uint32_t)(int)fma(-qq, pd, vd) & 0xFFu) << (8 * e);
+        }
+        w[t] = u;
+      }
+    if (a.ncorr > 0) {
+      const int64_t* c = a.corr64 + b * a.outplane + boff;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cv[e] = c[e];
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < kMaxP; ++t)
+      if (t < P) w[t] = *reinterpret_cast<const uint32_t*>(a.res8 + (b * P + t) * a.outplane + boff);
+  }
+  if (!kDeep && a.ncorr > 0) {
     const v4i c1 = *reinterpret_cast<const v4i*>(a.corr + (b * a.ncorr) * a.outplane + boff);
 #pragma unroll
     for (int e = 0; e < 4; ++e) cv[e] = c1[e];
@@ -977,7 +1068,9 @@ int run(const Call& c) {
   if (c.bits < 16 || c.bits > 53) return fail(FP64EMU_EINVAL, "bits must be in [16, 53]");
   if (c.batch < 0 || c.M < 0 || c.N < 0 || c.K < 0)
     return fail(FP64EMU_EINVAL, "shapes must be non-negative");
-  if (c.K > kMaxKSingle) return fail(FP64EMU_EINVAL, "K bound for int32 modular GEMM");
+  if (c.K > kMaxKSingle && (c.b_kn || c.ev))
+    return fail(FP64EMU_EINVAL, "K bound for int32 modular GEMM");
+  if (c.K > kMaxKDeep) return fail(FP64EMU_EINVAL, "K bound: 128 segments of 65536");
   fp64emu_layout_t L;
   make_layout(c.batch, c.M, c.N, c.K, c.P, c.corr, &L);
   const hipStream_t s = c.stream;
@@ -1039,12 +1132,27 @@ int run(const Call& c) {
   hipLaunchKernelGGL(pick_width_kernel, dim3(1), dim3(kThreads), 0, s, lgA, MF, lgB, NF,
                      std::min(tab.log2M, 126.0f), c.bits, sftA, sftB, bits_eff);
 
-  // 2. extraction (covers the padded planes entirely: no memset needed)
-  const int64_t nkt = L.Kp / kTileK;
-  if (nkt > 0) {
+  // 2-3. Per K segment (one unless deep): extraction (covers the padded
+  // planes entirely: no memset needed), then every modular GEMM in one launch.
+  GemmArgs ga;
+  ga.A = planesA; ga.B = planesB; ga.res8 = res8; ga.corr = corr;
+  ga.racc = L.deep ? reinterpret_cast<int32_t*>(res8) : nullptr;
+  ga.cacc = L.deep ? reinterpret_cast<int64_t*>(corr) : nullptr;
+  ga.memberA = L.memberA_bytes; ga.memberB = L.memberB_bytes;
+  ga.planeA = L.planeA_bytes; ga.planeB = L.planeB_bytes;
+  ga.outplane = L.outplane_bytes;
+  ga.TM = (int)(L.Mp / kTileR); ga.TN = (int)(L.Np / kTileR);
+  ga.P = c.P; ga.ncorr = L.ncorr; ga.nslots = c.P + L.ncorr; ga.batch = (int)c.batch;
+  for (int t = 0; t < kMaxP; ++t) { ga.p[t] = tab.p[t]; ga.invp[t] = tab.invp[t]; }
+  ga.total = (int64_t)ga.nslots * c.batch * ga.TM * ga.TN;
+  for (int seg = 0; seg < L.nseg; ++seg) {
+    const int64_t k0 = (int64_t)seg * L.kseg;
+    const int64_t kc = std::min<int64_t>(L.kseg, c.K - k0);
+    const int64_t nkt = round_up(kc, kTileK) / kTileK;
     ExtractArgs ea;
     ea.A = c.A; ea.B = c.B;
-    ea.M = c.M; ea.N = c.N; ea.K = c.K; ea.batch = c.batch;
+    ea.M = c.M; ea.N = c.N; ea.K = kc; ea.batch = c.batch;
+    ea.lda = c.K; ea.k0 = k0;
     ea.b_kn = c.b_kn ? 1 : 0;
     ea.use_corr = c.corr ? 1 : 0;
     ea.nkt = nkt;
@@ -1057,24 +1165,15 @@ int run(const Call& c) {
     ea.tab = tab;
     const int64_t wg = ea.wgA + c.batch * ea.rgB * nkt;
     hipLaunchKernelGGL(extract_kernel, dim3((unsigned)wg), dim3(kThreads), 0, s, ea);
-  }
-  if (c.ev) {
-    if (int st = check_hip(hipEventRecord(c.ev[1], s), "hipEventRecord")) return st;
-  }
-
-  // 3. modular GEMMs
-  {
-    GemmArgs ga;
-    ga.A = planesA; ga.B = planesB; ga.res8 = res8; ga.corr = corr;
-    ga.memberA = L.memberA_bytes; ga.memberB = L.memberB_bytes;
-    ga.planeA = L.planeA_bytes; ga.planeB = L.planeB_bytes;
-    ga.outplane = L.outplane_bytes;
+    if (c.ev) {
+      if (int st = check_hip(hipEventRecord(c.ev[1], s), "hipEventRecord")) return st;
+    }
     ga.nkt = (int)nkt;
-    ga.TM = (int)(L.Mp / kTileR); ga.TN = (int)(L.Np / kTileR);
-    ga.P = c.P; ga.ncorr = L.ncorr; ga.nslots = c.P + L.ncorr; ga.batch = (int)c.batch;
-    for (int t = 0; t < kMaxP; ++t) { ga.p[t] = tab.p[t]; ga.invp[t] = tab.invp[t]; }
-    ga.total = (int64_t)ga.nslots * c.batch * ga.TM * ga.TN;
-    hipLaunchKernelGGL(modgemm_kernel, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+    ga.first = seg == 0 ? 1 : 0;
+    if (L.deep)
+      hipLaunchKernelGGL(modgemm_kernel<true>, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+    else
+      hipLaunchKernelGGL(modgemm_kernel<false>, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
   }
   if (c.ev) {
     if (int st = check_hip(hipEventRecord(c.ev[2], s), "hipEventRecord")) return st;
@@ -1084,7 +1183,10 @@ int run(const Call& c) {
   // 4. reconstruction
   {
     ReconArgs ra;
-    ra.res8 = res8; ra.corr = corr; ra.out = c.out;
+    ra.res8 = res8; ra.corr = corr;
+    ra.res32 = reinterpret_cast<const int32_t*>(res8);
+    ra.corr64 = reinterpret_cast<const int64_t*>(corr);
+    ra.out = c.out;
     ra.sftA = sftA; ra.sftB = sftB; ra.bits_eff = bits_eff;
     ra.M = c.M; ra.N = c.N; ra.batch = c.batch; ra.outplane = L.outplane_bytes;
     ra.NB = L.Np / 32;
@@ -1093,10 +1195,17 @@ int run(const Call& c) {
     ra.ncorr = L.ncorr;
     ra.tab = tab;
     const unsigned grid = (unsigned)ra.nblocks;
-    if (c.exact)
-      hipLaunchKernelGGL(reconstruct_kernel<true>, dim3(grid), dim3(kThreads), 0, s, ra);
-    else
-      hipLaunchKernelGGL(reconstruct_kernel<false>, dim3(grid), dim3(kThreads), 0, s, ra);
+    if (L.deep) {
+      if (c.exact)
+        hipLaunchKernelGGL((reconstruct_kernel<true, true>), dim3(grid), dim3(kThreads), 0, s, ra);
+      else
+        hipLaunchKernelGGL((reconstruct_kernel<false, true>), dim3(grid), dim3(kThreads), 0, s, ra);
+    } else {
+      if (c.exact)
+        hipLaunchKernelGGL((reconstruct_kernel<true, false>), dim3(grid), dim3(kThreads), 0, s, ra);
+      else
+        hipLaunchKernelGGL((reconstruct_kernel<false, false>), dim3(grid), dim3(kThreads), 0, s, ra);
+    }
   }
   if (int st = check_hip(hipGetLastError(), "kernel launch")) return st;
   if (c.ev) {

@@ -17,6 +17,7 @@
 namespace {
 
 constexpr int64_t kMaxKSingle = 131071;
+constexpr int64_t kMaxKDeep = (int64_t)128 * 65536;   // K-segmented bound (mm, bmm)
 
 void check_status(int st) { TORCH_CHECK(st == FP64EMU_OK, fp64emu_last_error()); }
 
@@ -67,7 +68,8 @@ void fp64_emu_mm(at::Tensor& out, const at::Tensor& A, const at::Tensor& B,
   const int64_t M = A.size(0), K = A.size(1), N = B.size(0);
   TORCH_CHECK(B.size(1) == K, "expect B as [N, K]");
   check_out(out, A, {M, N}, "out f64 [M,N]");
-  TORCH_CHECK(K <= kMaxKSingle, "K bound for int32 modular GEMM");
+  // Deeper than 131071 runs K-segmented, to 128 segments of 65536.
+  TORCH_CHECK(K <= kMaxKDeep, "K bound: 128 segments of 65536");
   const c10::DeviceGuard guard(A.device());
   const std::vector<int32_t> pv = primes_vec(primes_cpu);
   const int P = (int)pv.size();
@@ -109,7 +111,7 @@ void fp64_emu_bmm(at::Tensor& out, const at::Tensor& A, const at::Tensor& B,
   const int64_t batch = A.size(0), M = A.size(1), K = A.size(2), N = B.size(1);
   TORCH_CHECK(B.size(0) == batch && B.size(2) == K, "expect B as [batch, N, K]");
   check_out(out, A, {batch, M, N}, "out f64 [batch,M,N]");
-  TORCH_CHECK(K <= kMaxKSingle, "K bound for int32 modular GEMM");
+  TORCH_CHECK(K <= kMaxKDeep, "K bound: 128 segments of 65536");
   const c10::DeviceGuard guard(A.device());
   const std::vector<int32_t> pv = primes_vec(primes_cpu);
   const int P = (int)pv.size();

@@ -28,7 +28,8 @@ EXPORTS = ("fp64emu_maxp", "fp64emu_last_error", "fp64emu_workspace_size", "fp64
 class Layout(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int64), ("M", ctypes.c_int64), ("N", ctypes.c_int64),
                 ("K", ctypes.c_int64), ("nprimes", ctypes.c_int), ("use_corr", ctypes.c_int),
-                ("ncorr", ctypes.c_int), ("nslab", ctypes.c_int), ("Mp", ctypes.c_int64),
+                ("ncorr", ctypes.c_int), ("nslab", ctypes.c_int), ("deep", ctypes.c_int),
+                ("nseg", ctypes.c_int), ("kseg", ctypes.c_int64), ("Mp", ctypes.c_int64),
                 ("Np", ctypes.c_int64), ("Kp", ctypes.c_int64), ("planeA_bytes", ctypes.c_int64),
                 ("planeB_bytes", ctypes.c_int64), ("memberA_bytes", ctypes.c_int64),
                 ("memberB_bytes", ctypes.c_int64), ("outplane_bytes", ctypes.c_int64)] + [

@@ -369,11 +369,13 @@ static double or_combine(const int* d, int P, const int32_t* primes, const int64
   return acc;
 }
 
-/* reconstruct_kernel<int8_t> (fp64_emu.cu:854-952) for one batch member:
- * res [P][M*N] int8, c1/c2 [M*N] int32 correction planes (NULL = none). */
-void or_reconstruct(const int8_t* res, const int32_t* c1, const int32_t* c2, int64_t M, int64_t N,
-                    const int32_t* primes, int P, int bits_eff, const int16_t* sftA,
-                    const int16_t* sftB, int exact, double* out) {
+/* reconstruct_kernel (fp64_emu.cu:854-952) for one batch member: res
+ * [P][M*N] int8; the correction as int32 planes c1/c2 or int64 planes
+ * d1/d2 (the K-segmented path's accumulators), NULL = none. */
+static void or_reconstruct_any(const int8_t* res, const int32_t* c1, const int32_t* c2,
+                               const int64_t* d1, const int64_t* d2, int64_t M, int64_t N,
+                               const int32_t* primes, int P, int bits_eff, const int16_t* sftA,
+                               const int16_t* sftB, int exact, double* out) {
   int32_t minv[OR_MAXP], mppack[OR_MAXP * OR_GROUPS];
   int64_t m64[2];
   float l2;
@@ -386,13 +388,93 @@ void or_reconstruct(const int8_t* res, const int32_t* c1, const int32_t* c2, int
       int r[OR_MAXP], d[OR_MAXP];
       for (int t = 0; t < P; t++) r[t] = res[(int64_t)t * total + idx];
       or_digits(r, P, primes, minv, mppack, d);
-      const long long corr = (c1 ? (long long)c1[idx] : 0LL) + (c2 ? (long long)c2[idx] : 0LL);
+      const long long corr = (c1 ? (long long)c1[idx] : 0LL) + (c2 ? (long long)c2[idx] : 0LL) +
+                             (d1 ? (long long)d1[idx] : 0LL) + (d2 ? (long long)d2[idx] : 0LL);
       const double v = or_combine(d, P, primes, m64, corr, cshift, exact);
       out[idx] = ldexp(v, -(int)sftA[i] - (int)sftB[j]);
     }
 }
 
-/* ---- whole pipeline: fp64_emu_cuda/fp64_emu.cu:1127-1407 (fused path) ---
+void or_reconstruct(const int8_t* res, const int32_t* c1, const int32_t* c2, int64_t M, int64_t N,
+                    const int32_t* primes, int P, int bits_eff, const int16_t* sftA,
+                    const int16_t* sftB, int exact, double* out) {
+  or_reconstruct_any(res, c1, c2, NULL, NULL, M, N, primes, P, bits_eff, sftA, sftB, exact, out);
+}
+
+void or_reconstruct64(const int8_t* res, const int64_t* d1, const int64_t* d2, int64_t M,
+                      int64_t N, const int32_t* primes, int P, int bits_eff, const int16_t* sftA,
+                      const int16_t* sftB, int exact, double* out) {
+  or_reconstruct_any(res, NULL, NULL, d1, d2, M, N, primes, P, bits_eff, sftA, sftB, exact, out);
+}
+
+/* Fold of the K-segmented residue sums (reduce_planes_kernel with kdepth =
+ * 1, fp64_emu.cu:833-847, 1570-1574): barrett_bal32 with the bias
+ * p * ceil((p/2)^2 / p), exact while |acc| <= that bias (at least 86 segments
+ * of balanced residues for every modulus). */
+int or_fold_residue(int32_t acc, int p) {
+  const uint64_t half = (uint64_t)(p / 2), maxabs = half * half;
+  const uint32_t bias = (uint32_t)((uint64_t)p * ((maxabs + (uint64_t)p - 1) / (uint64_t)p));
+  return or_barrett_bal32(acc, p, (uint32_t)((1u << 31) / (unsigned)p), bias);
+}
+
+/* One 65536-column segment of a row-major [R, K] int8 plane, made contiguous. */
+static void or_segment(const int8_t* src, int64_t R, int64_t K, int64_t k0, int64_t kc, int8_t* dst) {
+  for (int64_t r = 0; r < R; r++) memcpy(dst + r * kc, src + r * K + k0, (size_t)kc);
+}
+
+/* run_crt_bigk (fp64_emu.cu:1479-1579) for one batch member with B [N, K]:
+ * 65536-column segments; per segment the modular GEMMs give balanced int8
+ * residues, summed in int32, and the two int32 correction products, summed
+ * in int64; one fold to int8 and one reconstruction close the sum.
+ * Returns 0, or -1 on allocation failure. */
+static int or_mm_segmented(const int8_t* resA, const int8_t* hA, const int8_t* qA,
+                           const int8_t* resB, const int8_t* hB, const int8_t* qB, int64_t M,
+                           int64_t N, int64_t K, const int32_t* primes, int P, int use_corr,
+                           int nthreads, int be, const int16_t* sftA, const int16_t* sftB,
+                           int exact, double* out) {
+  const int64_t Kc = 65536;
+  const size_t pa = (size_t)M * K, pb = (size_t)N * K, po = (size_t)M * N;
+  int32_t* acc = (int32_t*)calloc(po * P + 1, sizeof(int32_t));
+  int64_t* d1 = (int64_t*)calloc(po + 1, sizeof(int64_t));
+  int64_t* d2 = (int64_t*)calloc(po + 1, sizeof(int64_t));
+  int8_t* sa = (int8_t*)malloc((size_t)M * Kc + 1);
+  int8_t* sb = (int8_t*)malloc((size_t)N * Kc + 1);
+  int8_t* sa2 = (int8_t*)malloc((size_t)M * Kc + 1);
+  int8_t* sb2 = (int8_t*)malloc((size_t)N * Kc + 1);
+  int8_t* r8 = (int8_t*)malloc(po + 1);
+  int32_t* c32 = (int32_t*)malloc(sizeof(int32_t) * po + 4);
+  int8_t* res8 = (int8_t*)malloc(po * P + 1);
+  int st = 0;
+  if (!acc || !d1 || !d2 || !sa || !sb || !sa2 || !sb2 || !r8 || !c32 || !res8) { st = -1; goto done; }
+  for (int64_t k0 = 0; k0 < K; k0 += Kc) {
+    const int64_t kc = K - k0 < Kc ? K - k0 : Kc;
+    for (int t = 0; t < P; t++) {
+      or_segment(resA + t * pa, M, K, k0, kc, sa);
+      or_segment(resB + t * pb, N, K, k0, kc, sb);
+      or_modgemm(sa, sb, M, N, kc, primes[t], r8, NULL, nthreads);
+      for (size_t i = 0; i < po; i++) acc[t * po + i] += r8[i];
+    }
+    if (use_corr) {
+      or_segment(hA, M, K, k0, kc, sa); or_segment(qB, N, K, k0, kc, sb);
+      or_segment(qA, M, K, k0, kc, sa2); or_segment(hB, N, K, k0, kc, sb2);
+      or_modgemm(sa, sb, M, N, kc, 0, NULL, c32, nthreads);      /* hi7_A q7_B^T */
+      for (size_t i = 0; i < po; i++) d1[i] += c32[i];
+      or_modgemm(sa2, sb2, M, N, kc, 0, NULL, c32, nthreads);    /* q7_A hi7_B^T */
+      for (size_t i = 0; i < po; i++) d2[i] += c32[i];
+    }
+  }
+  for (int t = 0; t < P; t++)
+    for (size_t i = 0; i < po; i++) res8[t * po + i] = (int8_t)or_fold_residue(acc[t * po + i], primes[t]);
+  or_reconstruct64(res8, use_corr ? d1 : NULL, use_corr ? d2 : NULL, M, N, primes, P, be, sftA,
+                   sftB, exact, out);
+done:
+  free(acc); free(d1); free(d2); free(sa); free(sb); free(sa2); free(sb2); free(r8); free(c32);
+  free(res8);
+  return st;
+}
+
+/* ---- whole pipeline: fp64_emu_cuda/fp64_emu.cu:1127-1407 (fused path),
+ * and 1479-1579 (K-segmented) for K > 131071 with B as [N, K] ---
  * A [batch, M, K]; B [batch, N, K] (b_kn = 0, mm/bmm) or [batch, K, N]
  * (b_kn = 1, mm_nt/bmm_nt).  Optional outputs (NULL to skip): the sizing
  * results after the width pick.  Returns 0, or -1 on allocation failure. */
@@ -438,6 +520,12 @@ int or_mm(double* out, const double* A, const double* B, int64_t batch, int64_t 
     or_extract_operand(A + b * M * K, 1, M, K, 0, sftA + b * M, be, primes, P, use_corr, resA, hA, qA);
     or_extract_operand(B + b * N * K, 1, N, K, b_kn, sftB + b * N, be, primes, P, use_corr, resB,
                        hB, qB);
+    if (K > 131071 && !b_kn) {
+      if (or_mm_segmented(resA, hA, qA, resB, hB, qB, M, N, K, primes, P, use_corr, nthreads, be,
+                          sftA + b * M, sftB + b * N, exact, out + b * M * N))
+        return -1;
+      continue;
+    }
     for (int t = 0; t < P; t++)
       or_modgemm(resA + t * pa, resB + t * pb, M, N, K, primes[t], res8 + t * po, NULL, nthreads);
     if (use_corr) {

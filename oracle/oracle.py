@@ -80,6 +80,9 @@ def lib():
         L.or_modgemm.argtypes = [vp, vp, i64, i64, i64, i32, vp, vp, i32]
         L.or_modgemm.restype = i32
         L.or_reconstruct.argtypes = [vp, vp, vp, i64, i64, vp, i32, i32, vp, vp, i32, vp]
+        L.or_reconstruct64.argtypes = [vp, vp, vp, i64, i64, vp, i32, i32, vp, vp, i32, vp]
+        L.or_fold_residue.argtypes = [ctypes.c_int32, i32]
+        L.or_fold_residue.restype = i32
         L.or_mm.argtypes = [vp, vp, vp, i64, i64, i64, i64, i32, vp, i32, i32, i32, i32, i32,
                             vp, vp, vp, vp, vp]
         L.or_mm.restype = i32
@@ -242,9 +245,29 @@ def reconstruct(res, c1, c2, primes, bits_eff, sftA, sftB, exact=True):
     return out
 
 
+def reconstruct64(res, d1, d2, primes, bits_eff, sftA, sftB, exact=True):
+    """reconstruct with int64 correction planes (the K-segmented path)."""
+    res = _c(res, np.int8)
+    P, M, N = res.shape
+    primes = _c(primes, np.int32)
+    d1 = _c(d1, np.int64) if d1 is not None else None
+    d2 = _c(d2, np.int64) if d2 is not None else None
+    out = np.zeros((M, N), np.float64)
+    lib().or_reconstruct64(_p(res), _p(d1), _p(d2), M, N, _p(primes), P, int(bits_eff),
+                           _p(_c(sftA, np.int16)), _p(_c(sftB, np.int16)), int(bool(exact)),
+                           _p(out))
+    return out
+
+
+def fold_residue(acc, p):
+    """The K-segmented path's fold of an int32 residue sum (barrett_bal32)."""
+    return lib().or_fold_residue(int(acc), int(p))
+
+
 def mm(A, B, b_kn, primes, exact=True, bits=53, use_corr=True, nthreads=0):
     """Whole pipeline.  A [batch,M,K] or [M,K]; B [batch,N,K] (b_kn=0) or
-    [batch,K,N] (b_kn=1).  Returns (out, sizing dict)."""
+    [batch,K,N] (b_kn=1).  K > 131071 with b_kn=0 runs the K-segmented path.
+    Returns (out, sizing dict)."""
     A = _c(A, np.float64)
     B = _c(B, np.float64)
     squeeze = A.ndim == 2

@@ -67,6 +67,7 @@ def test_maxp_and_status_codes():
 
 @pytest.mark.parametrize("shape", [(1, 1, 1, 1), (1, 128, 128, 4096), (1, 1023, 2049, 32769),
                                    (64, 512, 512, 512), (1, 300, 7, 65537), (3, 0, 5, 10),
+                                   (1, 48, 32, 200000), (2, 24, 16, 131072),
                                    (1, 8192, 8192, 8192)])
 @pytest.mark.parametrize("P,corr", [(14, True), (13, False), (20, True)])
 def test_layout_consistency(shape, P, corr):
@@ -75,8 +76,11 @@ def test_layout_consistency(shape, P, corr):
     assert L.Mp % 256 == 0 and L.Np % 256 == 0 and L.Kp % 64 == 0
     assert L.Mp >= max(M, 1) and L.Mp - max(M, 1) < 256
     assert L.Np >= max(N, 1) and L.Np - max(N, 1) < 256
-    assert L.Kp >= K and L.Kp - K < 64
-    assert L.ncorr == (0 if not corr else (1 if K <= 65536 else 2))
+    assert L.Kp >= L.kseg and L.Kp - L.kseg < 64
+    deep = K > 131071
+    assert L.deep == int(deep) and L.nseg == ((K + 65535) // 65536 if deep else 1)
+    assert L.kseg == (65536 if deep else K)
+    assert L.ncorr == (0 if not corr else (1 if (deep or K <= 65536) else 2))
     nplanes = P + (2 if corr else 0)
     assert L.planeA_bytes == L.Mp * L.Kp and L.planeB_bytes == L.Np * L.Kp
     assert L.memberA_bytes == nplanes * L.planeA_bytes
@@ -85,8 +89,9 @@ def test_layout_consistency(shape, P, corr):
     sizes = [("off_sftA", 2 * batch * M), ("off_sftB", 2 * batch * N), ("off_lgA", 4 * batch * M),
              ("off_lgB", 4 * batch * N), ("off_bits", 16), ("off_pmax", 8 * L.nslab * batch * N),
              ("off_pss", 8 * L.nslab * batch * N), ("off_planesA", batch * L.memberA_bytes),
-             ("off_planesB", batch * L.memberB_bytes), ("off_res8", batch * P * L.outplane_bytes),
-             ("off_corr", 4 * batch * L.ncorr * L.outplane_bytes)]
+             ("off_planesB", batch * L.memberB_bytes),
+             ("off_res8", (4 if deep else 1) * batch * P * L.outplane_bytes),
+             ("off_corr", (8 if deep else 4) * batch * L.ncorr * L.outplane_bytes)]
     prev_end = 0
     for name, size in sizes:
         off = getattr(L, name)
@@ -140,7 +145,10 @@ def test_validation_messages(kind):
     assert _call(kind, primes=[256, 128]) == (EINVAL, "moduli must be pairwise coprime")
     assert _call(kind, primes=[257, 255]) == (EINVAL, "moduli must be in [2, 256]")
     assert _call(kind, primes=[1]) == (EINVAL, "moduli must be in [2, 256]")
-    assert _call(kind, K=131072) == (EINVAL, "K bound for int32 modular GEMM")
+    if kind.endswith("_nt"):
+        assert _call(kind, K=131072) == (EINVAL, "K bound for int32 modular GEMM")
+    else:   # mm / bmm run K-segmented past 131071, to 128 segments of 65536
+        assert _call(kind, K=128 * 65536 + 1) == (EINVAL, "K bound: 128 segments of 65536")
     assert _call(kind, M=-1) == (EINVAL, "shapes must be non-negative")
     assert _call(kind, ws_bytes=100) == (EWORKSPACE, "workspace too small")
     assert _call(kind, null_ops=True)[0] == EINVAL

@@ -296,3 +296,41 @@ def test_beats_native_fp64(dev):
         return (time.perf_counter() - t0) / 4
 
     assert t(lambda: A @ Bt) / t(lambda: emu.mm_nt(A, Bt)) > 1.0
+
+
+def test_deep_k_integer_bitexact(dev):
+    """test_fp64_emu.py:122-131: K = 200000 (four 65536 segments), entries
+    in {-1, 0, 1}, exact at defaults."""
+    print("case deep_k_integer_bitexact", flush=True)
+    K = 200_000
+    A = _randint(-1, 2, (48, K), 41, dev)
+    B = _randint(-1, 2, (32, K), 42, dev)
+    ref = (A.cpu().long() @ B.cpu().long().T).double()
+    assert torch.equal(emu.mm(A, B).cpu(), ref)
+
+
+def test_deep_k_randn_accuracy(dev):
+    """test_fp64_emu.py:134-144 (>= 40 bits vs native), plus correct bits at
+    least native float64's against the double-double reference."""
+    print("case deep_k_randn_accuracy", flush=True)
+    K = 150_000
+    A = _randn((64, K), 43, dev)
+    B = _randn((48, K), 44, dev)
+    native = A @ B.t()
+    C = emu.mm(A, B)
+    assert _bits_vs(C, native) >= 40.0
+    assert _dd_bits(C, A, B.t().contiguous()) >= _dd_bits(native, A, B.t().contiguous())
+
+
+def test_deep_k_mm_nt_reroutes(dev):
+    """mm_nt / bmm_nt past the single-launch bound run as mm / bmm on the
+    transposed operand (torch-ext/fp64_emu/__init__.py:79-80, 121-122)."""
+    print("case deep_k_mm_nt_reroutes", flush=True)
+    K = 140_000
+    A = _randn((20, K), 45, dev)
+    Bt = _randn((K, 12), 46, dev)
+    assert torch.equal(emu.mm_nt(A, Bt), emu.mm(A, Bt.t().contiguous()))
+    assert torch.equal(emu.bmm_nt(A[None], Bt[None])[0], emu.mm(A, Bt.t().contiguous()))
+    with pytest.raises(RuntimeError, match="K bound for int32 modular GEMM"):
+        torch.ops.fp64_emu.fp64_emu_mm_nt(torch.empty(20, 12, dtype=torch.float64, device=dev),
+                                          A, Bt, *emu._tables(15), True, 53, True)

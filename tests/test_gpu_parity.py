@@ -81,3 +81,35 @@ def test_full_range_every_modulus_count(dev, P):
     B = 1 + 0.01 * torch.randn((512, 80), dtype=torch.float64, generator=g)
     B[:, ::5] *= -1
     check_call("mm_nt", A.to(dev), B.to(dev), O.PRIMES[:P], use_corr=P >= 12)
+
+
+DEEP_CASES = [
+    # kind, batch, M, N, K, nprimes, corr, exact
+    ("mm", 1, 40, 24, 140_000, 15, True, True),        # 3 segments, ragged last
+    ("mm", 1, 33, 17, 196_609, 16, True, True),        # last segment one column deep
+    ("mm", 1, 29, 31, 131_072, 15, False, True),       # first K past the single-launch bound
+    ("bmm", 2, 24, 16, 135_000, 15, True, False),
+]
+
+
+@pytest.mark.parametrize("kind,batch,M,N,K,P,corr,exact", DEEP_CASES)
+def test_deep_k_parity(dev, kind, batch, M, N, K, P, corr, exact):
+    """K-segmented path (K > 131071, B as [N, K]): sizing and the whole
+    output bit-exact against the oracle's segmented pipeline."""
+    from parity_util import bits_equal, oracle_sizing
+    from fp64_emu import capi
+    print(f"case deep-K {kind} b={batch} {M}x{N}x{K} P={P} corr={corr} exact={exact}", flush=True)
+    shapeA = (batch, M, K) if kind == "bmm" else (M, K)
+    shapeB = (batch, N, K) if kind == "bmm" else (N, K)
+    A = _randn(shapeA, K + M, dev)
+    B = _randn(shapeB, K + N, dev)
+    out, ws, lay = capi.run(kind, A, B, O.PRIMES[:P], exact=exact, use_corr=corr)
+    torch.cuda.synchronize()
+    assert lay.deep == 1 and lay.nseg == (K + 65535) // 65536
+    gsA, gsB, _, _, gbe = capi.sizing(ws[:lay.off_planesA].cpu().numpy(), lay)
+    Ah, Bh = A.cpu().numpy(), B.cpu().numpy()
+    obe, osA, osB, _, _ = oracle_sizing(Ah, Bh, False, O.PRIMES[:P], 53)
+    assert gbe == obe and np.array_equal(gsA, osA) and np.array_equal(gsB, osB)
+    oout, info = O.mm(Ah, Bh, 0, O.PRIMES[:P], exact=exact, use_corr=corr)
+    assert info["bits_eff"] == gbe
+    assert bits_equal(out.cpu().numpy(), oout), "deep-K output differs from the oracle"

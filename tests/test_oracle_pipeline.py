@@ -222,3 +222,50 @@ def test_inexact_recombine_close_to_exact():
     hi, lo = O.ddgemm_nt(A, np.ascontiguousarray(B.T))
     assert O.correct_bits(o2, hi, lo) >= 50.0
     assert np.max(np.abs(o1 - o2) / np.abs(hi).max()) < 2.0 ** -50
+
+
+def test_segment_fold_is_the_balanced_residue():
+    """The fold of K-segmented residue sums (barrett_bal32, bias
+    p ceil((p/2)^2/p)) equals the balanced residue of the sum over the
+    reachable range of up to 86 segments, for every modulus."""
+    for p in O.PRIMES:
+        lim = 86 * (p // 2)
+        for acc in list(range(-lim, lim + 1, 7)) + [-lim, lim, 0, 1, -1]:
+            assert O.fold_residue(acc, p) == O.balanced(acc, p), (p, acc)
+
+
+def test_deep_k_integer_bitexact():
+    """test_fp64_emu.py:122-131 re-expressed: K = 200000 entries in {-1,0,1}
+    through the K-segmented path (4 segments), exact."""
+    rng = np.random.default_rng(16)
+    K = 200_000
+    A = rng.integers(-1, 2, (12, K))
+    B = rng.integers(-1, 2, (8, K))
+    P, corr = O.plan_config(K)
+    out, _ = O.mm(A.astype(np.float64), B.astype(np.float64), 0, O.PRIMES[:P], use_corr=corr)
+    assert np.array_equal(out, (A @ B.T).astype(np.float64))
+
+
+def test_deep_k_segmentation_is_transparent():
+    """Segmented residues and int64 correction sums equal the single-pass
+    values computed with int64 products (numpy): the K-segmented output is
+    the full-depth CRT value."""
+    rng = np.random.default_rng(17)
+    K = 140_000
+    A = rng.standard_normal((6, K))
+    B = rng.standard_normal((5, K))
+    P = 15
+    pr = O.PRIMES[:P]
+    out, info = O.mm(A, B, 0, pr)
+    be = info["bits_eff"]
+    rA, hA, qA = O.extract_operand(A[None], 0, info["sftA"], be, pr)
+    rB, hB, qB = O.extract_operand(B[None], 0, info["sftB"], be, pr)
+    res = np.zeros((P, 6, 5), np.int8)
+    for t, p in enumerate(pr):
+        full = rA[0, t].astype(np.int64) @ rB[0, t].astype(np.int64).T
+        r = np.mod(full, p)
+        res[t] = np.where(r > (p - 1) // 2, r - p, r)
+    d1 = hA[0].astype(np.int64) @ qB[0].astype(np.int64).T
+    d2 = qA[0].astype(np.int64) @ hB[0].astype(np.int64).T
+    rec = O.reconstruct64(res, d1, d2, pr, be, info["sftA"], info["sftB"])
+    assert np.array_equal(out.view(np.uint64), rec.view(np.uint64))
