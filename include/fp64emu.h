@@ -64,7 +64,8 @@ const char* fp64emu_last_error(void);
 size_t fp64emu_workspace_size(int64_t batch, int64_t M, int64_t N, int64_t K,
                               int nprimes, int use_corr);
 
-/* out[M,N] = A[M,K] @ B[N,K]^T.   fp64_emu_cuda/fp64_emu.cu:1583-1608 */
+/* out[M,N] = A[M,K] @ B[N,K]^T; K up to 128 * 65536, K-segmented past 131071
+ * (fp64_emu_cuda/fp64_emu.cu:1479-1579).   fp64_emu_cuda/fp64_emu.cu:1583-1608 */
 int fp64emu_mm(double* out, const double* A, const double* B, int64_t M, int64_t N, int64_t K,
                const int32_t* primes /* host */, const int32_t* inv /* host, unused */,
                const int64_t* mu /* host, unused */, int nprimes, int exact, int64_t bits,
@@ -77,7 +78,8 @@ int fp64emu_mm_nt(double* out, const double* A, const double* Bt, int64_t M, int
                   int exact, int64_t bits, int use_corr, void* workspace, size_t workspace_bytes,
                   fp64emu_stream_t stream);
 
-/* out[b,M,N] = A[b,M,K] @ B[b,N,K]^T.   fp64_emu_cuda/fp64_emu.cu:1637-1662 */
+/* out[b,M,N] = A[b,M,K] @ B[b,N,K]^T; K as for fp64emu_mm.
+ * fp64_emu_cuda/fp64_emu.cu:1637-1662 */
 int fp64emu_bmm(double* out, const double* A, const double* B, int64_t batch, int64_t M, int64_t N,
                 int64_t K, const int32_t* primes, const int32_t* inv, const int64_t* mu,
                 int nprimes, int exact, int64_t bits, int use_corr, void* workspace,
