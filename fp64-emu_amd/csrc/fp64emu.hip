@@ -643,6 +643,61 @@ modgemm_kernel(GemmArgs g) {
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                                 \
     }                                                                                    \
   } while (0)
+  // Steady-state step (a copy for step kt+3 exists): an unconditional wait,
+  // so the compiler's own wait tracking sees every earlier fragment read
+  // retired (a conditional wait made it stall on the first read of each
+  // step), and the step in four fenced chunks, each {2 copies, 4 fragment
+  // reads, 8 MFMAs}: the copies reach the texture unit spread over the step
+  // instead of as a burst of 32 after the barrier, which delayed the last
+  // wave's MFMAs and made every wave wait for it at the next barrier.
+#define FP64EMU_DMA2(kt, c)                                                                  \
+  do {                                                                                       \
+    lds_i8* st_ = (lds_i8*)(lds + ((kt) & (kStages - 1)) * kStageBytes + wave * 4096 +       \
+                            ((c) >> 1) * kTileBytes);                                        \
+    const int8_t* g_ = (((c) >> 1) ? Bt : At) + (int64_t)(kt) * kTileBytes + goff;           \
+    __builtin_amdgcn_global_load_lds(g_, st_, 16, ((c) & 1) * 2048, 0);                      \
+    __builtin_amdgcn_global_load_lds(g_, st_, 16, ((c) & 1) * 2048 + 1024, 0);               \
+  } while (0)
+#define FP64EMU_READ4(F, kt, c)                                                              \
+  do {                                                                                       \
+    const v4i* sa_ = reinterpret_cast<const v4i*>(lds + ((kt) & (kStages - 1)) * kStageBytes); \
+    const v4i* sb_ = sa_ + kTileBytes / 16;                                                  \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                          \
+      const int f_ = (c) * 4 + j;                                                            \
+      if (f_ < 8) F[8 + f_] = sb_[(wn * 8 + f_) * 64 + lane];                                \
+      else F[f_ - 8] = sa_[(wm * 8 + f_ - 8) * 64 + lane];                                   \
+    }                                                                                        \
+  } while (0)
+#define FP64EMU_MMA8(F, c)                                                                   \
+  do {                                                                                       \
+    _Pragma("unroll") for (int xx = 0; xx < 2; ++xx)                                         \
+    _Pragma("unroll") for (int y = 0; y < 4; ++y) {                                          \
+      const int x = ((c) & 1) * 2 + xx, h = (c) >> 1;                                        \
+      acc[x][y] = __builtin_amdgcn_mfma_i32_32x32x32_i8(F[2 * x + h], F[8 + 2 * y + h],      \
+                                                         acc[x][y], 0, 0, 0);                \
+    }                                                                                        \
+  } while (0)
+#define FP64EMU_CHUNK(kt, FC, FN, c)                                                         \
+  do {                                                                                       \
+    FP64EMU_DMA2((kt) + 3, c);                                                               \
+    FP64EMU_READ4(FN, (kt) + 1, c);                                                          \
+    FP64EMU_MMA8(FC, c);                                                                     \
+    __builtin_amdgcn_sched_group_barrier(0x010, 2, 0);                                       \
+    _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                          \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                     \
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                                     \
+    }                                                                                        \
+    __builtin_amdgcn_sched_barrier(0);                                                       \
+  } while (0)
+#define FP64EMU_STEP_FULL(kt, FC, FN)                                                        \
+  do {                                                                                       \
+    wait_vm_lgkm0<kDmaPerStep>();                                                            \
+    barrier_lds();                                                                           \
+    FP64EMU_CHUNK(kt, FC, FN, 0);                                                            \
+    FP64EMU_CHUNK(kt, FC, FN, 1);                                                            \
+    FP64EMU_CHUNK(kt, FC, FN, 2);                                                            \
+    FP64EMU_CHUNK(kt, FC, FN, 3);                                                            \
+  } while (0)
 
   v16i acc[4][4];
 #pragma unroll
@@ -662,6 +717,10 @@ modgemm_kernel(GemmArgs g) {
   // Reading fragments of k-step nk (one past the end) touches a stale stage
   // and is never used; no copy targets it.
   int kt = 0;
+  for (; kt + 2 <= nk - 3; kt += 2) {        // copies for kt + 3 and kt + 4 exist
+    FP64EMU_STEP_FULL(kt, F0, F1);
+    FP64EMU_STEP_FULL(kt + 1, F1, F0);
+  }
   for (; kt + 2 <= nk; kt += 2) {
     FP64EMU_STEP(kt, F0, F1);
     FP64EMU_STEP(kt + 1, F1, F0);
@@ -676,6 +735,11 @@ modgemm_kernel(GemmArgs g) {
 #undef FP64EMU_READF
 #undef FP64EMU_MMA
 #undef FP64EMU_STEP
+#undef FP64EMU_DMA2
+#undef FP64EMU_READ4
+#undef FP64EMU_MMA8
+#undef FP64EMU_CHUNK
+#undef FP64EMU_STEP_FULL
 
   // Epilogue: 32x32 blocks (mb, nb) of this wave, 16 values per lane.
   const int64_t NB = (int64_t)g.TN * 8;                 // 32-blocks per output row
@@ -1313,7 +1377,9 @@ int fp64emu_mm_timed(double* out, float* times, const double* A, const double* B
   int created = 0;
   int st = FP64EMU_OK;
   for (; created < 5; ++created) {
-    st = check_hip(hipEventCreate(&ev[created]), "hipEventCreate");
+    // Timing-only events: no system-scope fence (cache writeback) on record.
+    st = check_hip(hipEventCreateWithFlags(&ev[created], hipEventDisableSystemFence),
+                   "hipEventCreate");
     if (st) break;
   }
   if (!st) {

@@ -144,19 +144,54 @@ def mm_timed(A, B, primes, exact=True, bits=53, use_corr=True):
     return out, list(times)
 
 
+_HIP = None
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000   # hip_runtime_api.h
+
+
+def _hip():
+    """The HIP runtime torch already loaded."""
+    global _HIP
+    if _HIP is None:
+        H = ctypes.CDLL("libamdhip64.so")
+        H.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        H.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                          ctypes.c_void_p]
+        H.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        _HIP = H
+    return _HIP
+
+
 class PhaseEvents:
-    """Five timing events for fp64emu_mm_nt_events, created through torch
-    on the current stream (recorded once so their HIP handles exist)."""
+    """Five timing events for fp64emu_mm_nt_events.  Created without the
+    system-scope fence on record (hipEventDisableSystemFence): a timing-only
+    event then costs no cache writeback and invalidation, which would
+    otherwise slow the work it brackets."""
 
     def __init__(self):
-        self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
-        for e in self.ev:
-            e.record()
-        self.handles = (ctypes.c_void_p * 5)(*[e.cuda_event for e in self.ev])
+        H = _hip()
+        self.handles = (ctypes.c_void_p * 5)()
+        for i in range(5):
+            ev = ctypes.c_void_p()
+            if H.hipEventCreateWithFlags(ctypes.byref(ev), HIP_EVENT_DISABLE_SYSTEM_FENCE) != 0:
+                raise CapiError("hipEventCreateWithFlags failed")
+            self.handles[i] = ev.value
 
     def phases_ms(self):
         """[sizing+extract, gemms, 0-marker, reconstruct] after a sync."""
-        return [self.ev[i].elapsed_time(self.ev[i + 1]) for i in range(4)]
+        H = _hip()
+        out = []
+        for i in range(4):
+            t = ctypes.c_float()
+            if H.hipEventElapsedTime(ctypes.byref(t), self.handles[i], self.handles[i + 1]) != 0:
+                raise CapiError("hipEventElapsedTime failed")
+            out.append(t.value)
+        return out
+
+    def __del__(self):
+        if _HIP is not None:
+            for h in self.handles:
+                if h:
+                    _HIP.hipEventDestroy(h)
 
 
 def mm_nt_events(A, Bt, primes, out, ws, events, exact=True, bits=53, use_corr=True):
