@@ -204,7 +204,19 @@ size_rows_kernel(const double* __restrict__ A, int64_t rowsA, const double* __re
   const double* __restrict__ x = (isA ? A : B) + r * K;
   const int tid = threadIdx.x;
   double mx = 0.0, ss = 0.0;
-  for (int64_t c = tid; c < K; c += kThreads) {
+  // Loads go out eight at a time; the fma chain keeps the reference's order.
+  int64_t c = tid;
+  for (; c + 7 * kThreads < K; c += 8 * kThreads) {
+    double v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = x[c + u * kThreads];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      mx = fmax(mx, fabs(v[u]));
+      ss = fma(v[u], v[u], ss);
+    }
+  }
+  for (; c < K; c += kThreads) {
     const double v = x[c];
     mx = fmax(mx, fabs(v));
     ss = fma(v, v, ss);
@@ -241,7 +253,19 @@ size_cols_partial_kernel(const double* __restrict__ X, int64_t totalcols, int64_
   const int64_t k1 = min(k0 + kslab, rows_per);
   const double* __restrict__ base = X + b * rows_per * cols_per + n;
   double mx = 0.0, ss = 0.0;
-  for (int64_t k = k0; k < k1; ++k) {
+  // Sixteen rows in flight per thread; the fma chain keeps the slab order.
+  int64_t k = k0;
+  for (; k + 16 <= k1; k += 16) {
+    double v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = base[(k + u) * cols_per];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      mx = fmax(mx, fabs(v[u]));
+      ss = fma(v[u], v[u], ss);
+    }
+  }
+  for (; k < k1; ++k) {
     const double v = base[k * cols_per];
     mx = fmax(mx, fabs(v));
     ss = fma(v, v, ss);
@@ -268,20 +292,40 @@ size_cols_final_kernel(const double* __restrict__ pmax, const double* __restrict
 // Width pick: g = floor((log2M - 1 - (max lgA + max lgB + 0.5)) / 2),
 // g <= 53 - bits, be = max(bits + g, 16); g folded into every shift and be
 // kept on the device.  fp64_emu_cuda/fp64_emu.cu:191-231.
-__global__ void __launch_bounds__(kThreads)
+constexpr int kPickThreads = 1024;
+
+__global__ void __launch_bounds__(kPickThreads)
 pick_width_kernel(const float* __restrict__ lgA, int64_t m, const float* __restrict__ lgB,
                   int64_t n, float log2M, int bits, int16_t* __restrict__ sftA,
                   int16_t* __restrict__ sftB, int* __restrict__ bits_eff) {
-  __shared__ float sa[kThreads], sb[kThreads];
+  constexpr int T = kPickThreads;
+  __shared__ float sa[T], sb[T];
   __shared__ int s_g;
   const int tid = threadIdx.x;
   float a = -INFINITY, b = -INFINITY;
-  for (int64_t i = tid; i < m; i += kThreads) a = fmaxf(a, lgA[i]);
-  for (int64_t j = tid; j < n; j += kThreads) b = fmaxf(b, lgB[j]);
+  // Eight independent loads in flight per thread (a max is order-free).
+  int64_t i = tid;
+  for (; i + 7 * T < m; i += 8 * T) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = lgA[i + u * T];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a = fmaxf(a, v[u]);
+  }
+  for (; i < m; i += T) a = fmaxf(a, lgA[i]);
+  int64_t j = tid;
+  for (; j + 7 * T < n; j += 8 * T) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = lgB[j + u * T];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) b = fmaxf(b, v[u]);
+  }
+  for (; j < n; j += T) b = fmaxf(b, lgB[j]);
   sa[tid] = a;
   sb[tid] = b;
   __syncthreads();
-  for (int s = kThreads / 2; s > 0; s >>= 1) {
+  for (int s = T / 2; s > 0; s >>= 1) {
     if (tid < s) {
       sa[tid] = fmaxf(sa[tid], sa[tid + s]);
       sb[tid] = fmaxf(sb[tid], sb[tid + s]);
@@ -300,15 +344,16 @@ pick_width_kernel(const float* __restrict__ lgA, int64_t m, const float* __restr
   __syncthreads();
   const int g = s_g;
   if (g != 0) {
-    for (int64_t i = tid; i < m; i += kThreads) sftA[i] = (int16_t)(sftA[i] + g);
-    for (int64_t j = tid; j < n; j += kThreads) sftB[j] = (int16_t)(sftB[j] + g);
+    for (int64_t q = tid; q < m; q += T) sftA[q] = (int16_t)(sftA[q] + g);
+    for (int64_t q = tid; q < n; q += T) sftB[q] = (int16_t)(sftB[q] + g);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Extraction.  Element semantics follow fp64_emu_cuda/fp64_emu.cu:288-321
-// (integer-only RNE scaling of the IEEE encoding, hi7/q7 correction
-// summaries); the residue reduction is this build's: the signed integer
+// (RNE scaling of |x| by 2^shift, hi7/q7 correction summaries), computed
+// here with exact power-of-two fp64 operations instead of integer shifts of
+// the IEEE encoding; the residue reduction is this build's: the signed integer
 // td = +-round(|x| 2^s) splits as th * 2^27 + tl (th signed, tl < 2^27),
 // v = th * (2^27 mod p) + tl is exact in fp64 (|v| < 2^35), and
 // r = v - p * RNE(v / p) is exact: the quotient error (< 2^-26) stays far
@@ -323,16 +368,6 @@ pick_width_kernel(const float* __restrict__ lgA, int64_t m, const float* __restr
 // k % 16 at byte 16 * l + k % 16.  The correction plane is one 2*Kp-deep
 // plane: A = [hi7 | q7], B = [q7 | hi7], so one GEMM accumulates
 // hi7_A q7_B^T + q7_A hi7_B^T.
-
-__device__ __forceinline__ uint64_t rne_shift_right(uint64_t mag, int s) {
-  if (s <= 0) return (s > -64) ? (mag << (-s)) : 0ull;
-  if (s > 63) return 0ull;
-  const uint64_t kept = mag >> s;
-  const uint64_t dropped = mag - (kept << s);
-  const uint64_t half = 1ull << (s - 1);
-  const bool up = (dropped > half) || (dropped == half && (kept & 1ull));
-  return kept + (up ? 1ull : 0ull);
-}
 
 struct ExtractArgs {
   const double* A;
@@ -409,32 +444,32 @@ extract_kernel(ExtractArgs a) {
     }
   }
 
-  // Split every element first: th, tl as exact doubles, hi7/q7 bytes.
+  // Split every element first: th, tl as exact doubles, hi7/q7 bytes.  All
+  // scalings are by powers of two and exact: y = |x| 2^shift (< 2^be, or
+  // rounds to a subnormal far below 1/2, whose rounding is then 0 anyway),
+  // Tu = RNE(y) is the integer-only RNE of the reference, d = y - Tu is exact
+  // (|d| <= 1/2), and RNE(256 y) - 256 Tu = RNE(256 d) because 256 Tu is even,
+  // so the tie parity is unchanged.  td = +-Tu splits as th 2^27 + tl with
+  // th = floor(td / 2^27) and tl in [0, 2^27), both exact.
   double th[16], tl[16];
   uint32_t hw[4] = {0u, 0u, 0u, 0u}, qw[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int jj = 0; jj < 16; ++jj) {
-    const uint64_t xb = (uint64_t)__double_as_longlong(x[jj]);
-    const bool neg = (xb >> 63) != 0;
-    const int e = (int)((xb >> 52) & 0x7FF);
-    const uint64_t mant = xb & 0xFFFFFFFFFFFFFull;
-    const uint64_t mag = e ? (mant | (1ull << 52)) : mant;
-    // |x| * 2^shift = mag * 2^(t - 52); subnormals read as exponent 1.
-    const int t = (e ? e : 1) - 1075 + shift + 52;
-    const uint64_t Tu = rne_shift_right(mag, 52 - t);
-    const int64_t td = neg ? -(int64_t)Tu : (int64_t)Tu;
+    const double y = ldexp(fabs(x[jj]), shift);
+    const double Tu = rint(y);
+    const double td = copysign(Tu, x[jj]);
     if (a.use_corr) {
-      const int64_t r8 = (int64_t)rne_shift_right(mag, 44 - t) - (int64_t)(Tu << 8);
-      const int64_t h8 = (int64_t)rne_shift_right(Tu, be - 7);
-      int64_t hs = neg ? -h8 : h8, qs = neg ? -r8 : r8;
-      hs = hs > 127 ? 127 : (hs < -127 ? -127 : hs);
-      qs = qs > 127 ? 127 : (qs < -127 ? -127 : qs);
+      const double h8 = rint(ldexp(Tu, 7 - be));
+      const double r8 = rint(ldexp(y - Tu, 8));
+      const bool neg = signbit(x[jj]);
+      const int hs = (int)fmin(fmax(neg ? -h8 : h8, -127.0), 127.0);   // h8 >= 0
+      const int qs = (int)fmin(fmax(neg ? -r8 : r8, -127.0), 127.0);   // r8 signed
       hw[jj >> 2] |= ((uint32_t)hs & 0xFFu) << (8 * (jj & 3));
       qw[jj >> 2] |= ((uint32_t)qs & 0xFFu) << (8 * (jj & 3));
     }
-    const int64_t hi = td >> 27;                   // arithmetic: floor(td / 2^27)
-    th[jj] = (double)hi;
-    tl[jj] = (double)(td - (hi << 27));            // in [0, 2^27)
+    const double hi = floor(ldexp(td, -27));
+    th[jj] = hi;
+    tl[jj] = fma(-hi, 134217728.0, td);            // in [0, 2^27)
   }
 
   // One plane at a time: 16 residues -> one 16-byte chunk per lane, 1 KiB
@@ -1193,7 +1228,7 @@ int run(const Call& c) {
     hipLaunchKernelGGL(size_cols_final_kernel, dim3(gcx), dim3(kThreads), 0, s, pmax, pss, NF,
                        nslab, c.bits, sftB, lgB);
   }
-  hipLaunchKernelGGL(pick_width_kernel, dim3(1), dim3(kThreads), 0, s, lgA, MF, lgB, NF,
+  hipLaunchKernelGGL(pick_width_kernel, dim3(1), dim3(kPickThreads), 0, s, lgA, MF, lgB, NF,
                      std::min(tab.log2M, 126.0f), c.bits, sftA, sftB, bits_eff);
 
   // 2-3. Per K segment (one unless deep): extraction (covers the padded
