@@ -51,6 +51,8 @@ constexpr int64_t kMaxKDeep = 128 * kSegK;       // the reference's segmented bo
 // x + kMagic (|x| < 2^51) lands on the integer grid of [2^52, 2^53): the sum
 // rounds x to the nearest integer, ties to even.
 constexpr double kMagic = 6755399441055744.0;
+// 1/2 + 2^-20: floor(y RN(1/p) + kHalfUp) = floor(y/p + 1/2) for |y| < 2^27.
+constexpr double kHalfUp = 0.5 + 0x1p-20;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -917,7 +919,9 @@ struct ReconArgs {
   ModTables tab;
 };
 
-template <bool kExact, bool kDeep>
+// kP: the modulus count fixed at compile time (0: read from the tables), so
+// the digit loops unroll to exactly P steps without guards.
+template <bool kExact, bool kDeep, int kP>
 __global__ void __launch_bounds__(kThreads)
 reconstruct_kernel(ReconArgs a) {
   const int64_t blk = blockIdx.x;
@@ -932,7 +936,7 @@ reconstruct_kernel(ReconArgs a) {
   const int64_t j = nb * 32 + (l & 31);
   if (j >= a.N || i0 >= a.M) return;
 
-  const int P = a.tab.P;
+  const int P = kP > 0 ? kP : a.tab.P;
   const int64_t boff = (mb * a.NB + nb) * 1024 + 4 * thr;  // byte (int8) / element (int32)
   uint32_t w[kMaxP];
   int64_t cv[4] = {0, 0, 0, 0};
@@ -987,10 +991,13 @@ reconstruct_kernel(ReconArgs a) {
     const int pt = a.tab.p[t];
     pv[t] = pt;
     if (t == 0) {
-      // M_0 = 1: the first digit is the (balanced) residue itself.
+      // M_0 = 1: the first digit is the residue itself, brought into
+      // [-p/2, (p-1)/2] (a no-op for p = 256, whose bytes are that range).
+      const double pd0 = (double)pt, ip0 = a.tab.invp[0];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int d = (int)(int8_t)(uint8_t)(w[0] >> (8 * e));
+        const double rd = (double)(int)(int8_t)(uint8_t)(w[0] >> (8 * e));
+        const int d = (int)fma(-floor(fma(rd, ip0, kHalfUp)), pd0, rd);
         dg[e][0] = d;
         dp[e][0] = (int)((uint32_t)d & 0xFFu);
       }
@@ -1009,15 +1016,12 @@ reconstruct_kernel(ReconArgs a) {
       for (int g = 0; g < kGarnerWords; ++g)
         if (4 * g < t) acc = __builtin_amdgcn_sdot4(dp[e][g], mpw[g], acc, false);
       const double yd = (double)__mul24(rt - acc, mi);  // |y| < 2^27, 24-bit operands
-      const double qq = fma(yd, ip, kMagic) - kMagic;   // exact nearest quotient
+      // d = y - p floor(y/p + 1/2): the offset 2^-20 outweighs the rounding
+      // of y RN(1/p) (< 2^-26) and stays far below the gap 1/p to the next
+      // integer, so d lies in [-p/2, (p-1)/2] for odd and even p alike
+      // (barrett_bal32's range) with no tie fixup.
+      const double qq = floor(fma(yd, ip, kHalfUp));
       dg[e][t] = (int)fma(-qq, pd, yd);
-    }
-    // Even modulus (uniform branch): the nearest quotient can leave +p/2,
-    // whose balanced representative is -p/2.
-    if ((pt & 1) == 0) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (dg[e][t] == (pt >> 1)) dg[e][t] -= pt;
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e)
@@ -1162,6 +1166,31 @@ int validate_primes(const int32_t* primes, int P) {
   return FP64EMU_OK;
 }
 
+// Modulus counts of the planner (plan_config: 14-15; plan: up to 20) get a
+// reconstruction compiled for their exact count; others use the generic one.
+template <bool kExact>
+void launch_reconstruct_p(int P, unsigned grid, hipStream_t s, const ReconArgs& ra) {
+  switch (P) {
+#define FP64EMU_RECON_CASE(n)                                                                 \
+    case n:                                                                                   \
+      hipLaunchKernelGGL((reconstruct_kernel<kExact, false, n>), dim3(grid), dim3(kThreads),  \
+                         0, s, ra);                                                           \
+      return;
+    FP64EMU_RECON_CASE(12) FP64EMU_RECON_CASE(13) FP64EMU_RECON_CASE(14)
+    FP64EMU_RECON_CASE(15) FP64EMU_RECON_CASE(16) FP64EMU_RECON_CASE(17)
+    FP64EMU_RECON_CASE(18) FP64EMU_RECON_CASE(19) FP64EMU_RECON_CASE(20)
+#undef FP64EMU_RECON_CASE
+    default:
+      hipLaunchKernelGGL((reconstruct_kernel<kExact, false, 0>), dim3(grid), dim3(kThreads), 0,
+                         s, ra);
+  }
+}
+
+void launch_reconstruct(bool exact, int P, unsigned grid, hipStream_t s, const ReconArgs& ra) {
+  if (exact) launch_reconstruct_p<true>(P, grid, s, ra);
+  else launch_reconstruct_p<false>(P, grid, s, ra);
+}
+
 int run(const Call& c) {
   if (int st = validate_primes(c.primes, c.P)) return st;
   if (c.bits < 16 || c.bits > 53) return fail(FP64EMU_EINVAL, "bits must be in [16, 53]");
@@ -1296,14 +1325,11 @@ int run(const Call& c) {
     const unsigned grid = (unsigned)ra.nblocks;
     if (L.deep) {
       if (c.exact)
-        hipLaunchKernelGGL((reconstruct_kernel<true, true>), dim3(grid), dim3(kThreads), 0, s, ra);
+        hipLaunchKernelGGL((reconstruct_kernel<true, true, 0>), dim3(grid), dim3(kThreads), 0, s, ra);
       else
-        hipLaunchKernelGGL((reconstruct_kernel<false, true>), dim3(grid), dim3(kThreads), 0, s, ra);
+        hipLaunchKernelGGL((reconstruct_kernel<false, true, 0>), dim3(grid), dim3(kThreads), 0, s, ra);
     } else {
-      if (c.exact)
-        hipLaunchKernelGGL((reconstruct_kernel<true, false>), dim3(grid), dim3(kThreads), 0, s, ra);
-      else
-        hipLaunchKernelGGL((reconstruct_kernel<false, false>), dim3(grid), dim3(kThreads), 0, s, ra);
+      launch_reconstruct(c.exact, c.P, grid, s, ra);
     }
   }
   if (int st = check_hip(hipGetLastError(), "kernel launch")) return st;
