@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--n", type=int, default=8192)
     ap.add_argument("--no-accuracy", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--configs", action="store_true",
+                    help="instead of the headline line, one JSON line per BASELINE config "
+                         "(c1, c2, c3a, c3b, c4, c5 default and reduced)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a float64 streaming kernel over 1 GiB (read 1 GiB, write "
                          "1 GiB) three times: the scale of the FETCH_SIZE / WRITE_SIZE counters")
@@ -72,6 +75,9 @@ def main():
 
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.configs:
+        run_configs(max(args.steps, 3), max(args.warmup, 1))
         return
 
     import torch
@@ -203,6 +209,110 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
+
+
+def _config_inputs(name, torch):
+    """Inputs of the BASELINE configs, generated on the CPU (seeds 1000 cfg,
+    1000 cfg + 1)."""
+    g = lambda seed: torch.Generator().manual_seed(seed)  # noqa: E731
+    if name == "c1":
+        return "mm_nt", torch.randn(128, 4096, dtype=torch.float64, generator=g(1000)), \
+            torch.randn(4096, 128, dtype=torch.float64, generator=g(1001)), None
+    if name == "c2":
+        return "mm_nt", torch.randn(8192, 8192, dtype=torch.float64, generator=g(2000)), \
+            torch.randn(8192, 8192, dtype=torch.float64, generator=g(2001)), None
+    if name == "c3a":
+        def wide(seed):
+            gg = g(seed)
+            sgn = torch.randint(0, 2, (4096, 4096), generator=gg) * 2 - 1
+            m = 1 + torch.rand(4096, 4096, generator=gg, dtype=torch.float64)
+            e = torch.randint(-20, 21, (4096, 4096), generator=gg)
+            return sgn * torch.ldexp(m, e)
+        return "mm_nt", wide(3000), wide(3001), None
+    if name == "c3b":
+        r = lambda seed: torch.randint(-2 ** 20, 2 ** 20 + 1, (4096, 4096), generator=g(seed)).double()  # noqa: E731
+        return "mm_nt", r(3100), r(3101), None
+    if name == "c4":
+        return "bmm_nt", torch.randn(64, 512, 512, dtype=torch.float64, generator=g(4000)), \
+            torch.randn(64, 512, 512, dtype=torch.float64, generator=g(4001)), None
+    u = lambda shape, seed: torch.rand(shape, dtype=torch.float64, generator=g(seed)) * 2 - 1  # noqa: E731
+    A, B = u((1023, 32769), 5000), u((32769, 2049), 5001)
+    return "mm_nt", A, B, ((13, False) if name == "c5r" else None)
+
+
+def run_configs(steps, warmup):
+    """One JSON line per BASELINE config: effective FP64 TFLOPS, the
+    plan-adjusted INT8 roofline fraction, per-phase ms (mm_nt forms), the
+    native float64 comparator and correct bits against the device
+    double-double GEMM."""
+    import torch
+    import fp64_emu
+    from fp64_emu import capi
+    dev = torch.device("cuda:0")
+    for name in ("c1", "c2", "c3a", "c3b", "c4", "c5", "c5r"):
+        kind, A, B, plan = _config_inputs(name, torch)
+        A, B = A.to(dev), B.to(dev)
+        batched = kind == "bmm_nt"
+        K = A.shape[-1]
+        P, corr = plan if plan else fp64_emu.plan_config(K)
+        G = P + (2 if corr else 0)
+        M, N = A.shape[-2], B.shape[-1]
+        batch = A.shape[0] if batched else 1
+        flop = 2.0 * batch * M * N * K
+        emu = (lambda: fp64_emu.bmm_nt(A, B, nprimes=P, corr=corr)) if batched else \
+            (lambda: fp64_emu.mm_nt(A, B, nprimes=P, corr=corr))
+        nat = (lambda: torch.bmm(A, B)) if batched else (lambda: A @ B)
+
+        def timed(fn):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e3 / steps
+
+        ms = timed(emu)
+        nat_ms = timed(nat)
+        phases = None
+        if not batched:
+            primes = fp64_emu._PRIMES[:P]
+            lay = capi.layout(1, M, N, K, P, corr)
+            ws = torch.empty(int(lay.total), dtype=torch.uint8, device=dev)
+            C = torch.empty(M, N, dtype=torch.float64, device=dev)
+            evs = [capi.PhaseEvents() for _ in range(steps)]
+            for i in range(steps):
+                capi.mm_nt_events(A, B, primes, C, ws, evs[i], use_corr=corr)
+            torch.cuda.synchronize()
+            ph = [e.phases_ms() for e in evs]
+            phases = [round(sum(p[i] for p in ph) / len(ph), 4) for i in range(4)]
+            del ws, C, evs
+        Ce, Cn = emu(), nat()
+        bits = {}
+        for tag, X in (("emu", Ce), ("native", Cn)):
+            errs, scale = 0.0, 0.0
+            for b in range(batch):
+                Ab = A[b] if batched else A
+                Bb = B[b] if batched else B
+                hi, lo = capi.ddgemm_nt(Ab, Bb.t().contiguous())
+                Xb = X[b] if batched else X
+                errs = max(errs, ((Xb - hi) - lo).abs().max().item())
+                scale = max(scale, hi.abs().max().item())
+                if batched and b >= 7:
+                    break            # 8 members suffice for the correct-bit estimate
+            bits[tag] = 53.0 if errs == 0 else round(-math.log2(errs / scale), 2)
+        value = flop / (ms * 1e-3) / 1e12
+        rec = {"config": name, "kind": kind, "batch": batch, "M": M, "N": N, "K": K,
+               "nprimes": P, "corr": corr, "gemms": G, "ms": round(ms, 4),
+               "tflops": round(value, 2),
+               "plan_roofline_frac": round(value / (INT8_PEAK_TOPS / G), 4),
+               "phases_ms": phases, "native_ms": round(nat_ms, 4),
+               "native_tflops": round(flop / (nat_ms * 1e-3) / 1e12, 2),
+               "correct_bits_emu": bits["emu"], "correct_bits_native": bits["native"]}
+        print(json.dumps(rec), flush=True)
+        del A, B, Ce, Cn
+        torch.cuda.empty_cache()
 
 
 def cpu_baseline(A, Bt, P, corr):

@@ -139,6 +139,29 @@ void slab_split(int64_t NF, int64_t K, int64_t* kslab, int* nslab) {
   *nslab = (int)((K + *kslab - 1) / *kslab);
 }
 
+// GEMM K-split.  Output tiles x slots are the GEMM's work items; when they
+// are few against the 256 CUs (small or skinny products), S groups per tile
+// each take a contiguous K range, and reconstruction sums the S residue
+// (and correction) planes.  S minimises the estimated makespan
+// ceil(items S / 256) (k-steps per group + a fixed cost per group), keeping
+// at least 8 k-steps per group.  A function of the shapes only, so the
+// workspace size is too.
+constexpr int kCUs = 256;
+constexpr int kMaxSplit = 16;
+
+int choose_ksplit(int64_t batch, int64_t tiles, int64_t nkt, int P, int ncorr) {
+  const int64_t items = batch * tiles * (P + (ncorr == 1 ? 2 : ncorr));  // fused corr: 2x deep
+  int best = 1;
+  double best_t = 1e300;
+  for (int S = 1; S <= kMaxSplit; S *= 2) {
+    if (S > 1 && nkt / S < 8) break;
+    const double steps = (double)((nkt + S - 1) / S) + 6.0;
+    const double t = (double)((items * S + kCUs - 1) / kCUs) * steps;
+    if (t < best_t * 0.97) { best_t = t; best = S; }
+  }
+  return best;
+}
+
 void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool corr,
                  fp64emu_layout_t* L) {
   std::memset(L, 0, sizeof(*L));
@@ -163,6 +186,8 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   L->memberA_bytes = (int64_t)nplanes * L->planeA_bytes;
   L->memberB_bytes = (int64_t)nplanes * L->planeB_bytes;
   L->outplane_bytes = L->Mp * L->Np;
+  L->ksplit = L->deep ? 1 : choose_ksplit(batch, (L->Mp / kTileR) * (L->Np / kTileR),
+                                          L->Kp / kTileK, P, L->ncorr);
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o = align_up(o + bytes); return at; };
   L->off_sftA = take(sizeof(int16_t) * batch * M);
@@ -174,9 +199,10 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   L->off_pss = take(sizeof(double) * (size_t)nslab * batch * N);
   L->off_planesA = take((size_t)(batch * L->memberA_bytes));
   L->off_planesB = take((size_t)(batch * L->memberB_bytes));
-  L->off_res8 = take((L->deep ? sizeof(int32_t) : 1) * (size_t)(batch * P * L->outplane_bytes));
+  L->off_res8 = take((L->deep ? sizeof(int32_t) : 1) *
+                     (size_t)(L->ksplit * batch * P * L->outplane_bytes));
   L->off_corr = take((L->deep ? sizeof(int64_t) : sizeof(int32_t)) *
-                     (size_t)(batch * L->ncorr * L->outplane_bytes));
+                     (size_t)(L->ksplit * batch * L->ncorr * L->outplane_bytes));
   L->total = o;
 }
 
@@ -284,7 +310,22 @@ size_cols_final_kernel(const double* __restrict__ pmax, const double* __restrict
   const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (j >= totalcols) return;
   double mx = 0.0, ss = 0.0;
-  for (int s = 0; s < nslab; ++s) {
+  // Eight slabs' loads in flight; the sum keeps the slab order.
+  int s = 0;
+  for (; s + 8 <= nslab; s += 8) {
+    double vm[8], vs[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      vm[u] = pmax[(int64_t)(s + u) * totalcols + j];
+      vs[u] = pss[(int64_t)(s + u) * totalcols + j];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      mx = fmax(mx, vm[u]);
+      ss = ss + vs[u];
+    }
+  }
+  for (; s < nslab; ++s) {
     mx = fmax(mx, pmax[(int64_t)s * totalcols + j]);
     ss = ss + pss[(int64_t)s * totalcols + j];
   }
@@ -548,6 +589,7 @@ struct GemmArgs {
   int nkt;             // k tiles of a residue plane
   int TM, TN;          // 256-tiles per member
   int P, ncorr, nslots, batch;
+  int ksplit;          // groups per output tile, each over a contiguous K range
   int p[kMaxP];
   double invp[kMaxP];
 };
@@ -602,8 +644,10 @@ modgemm_kernel(GemmArgs g) {
   int64_t L = i;
   if ((i >> 8) < (g.total >> 8)) L = (i & ~255ll) + (i & 7) * 32 + ((i & 255) >> 3);
   const int64_t tiles = (int64_t)g.TM * g.TN;
-  const int64_t sb = L / tiles;
-  const int tile = (int)(L - sb * tiles);
+  const int64_t sbs = L / tiles;                       // (slot, member, split)
+  const int tile = (int)(L - sbs * tiles);
+  const int split = (int)(sbs % g.ksplit);
+  const int64_t sb = sbs / g.ksplit;
   const int slot = (int)(sb / g.batch);
   const int64_t b = sb - (int64_t)slot * g.batch;
   // Grouped tile order: 8 row tiles per group, column-major inside.
@@ -619,8 +663,12 @@ modgemm_kernel(GemmArgs g) {
   const bool is_corr = slot < g.ncorr;
   const int plane = is_corr ? g.P : slot - g.ncorr;
   const int rstride = is_corr ? 2 * g.nkt : g.nkt;           // k tiles per row tile
-  const int kt0 = (is_corr && g.ncorr == 2) ? slot * g.nkt : 0;
-  const int nk = is_corr ? (g.ncorr == 1 ? 2 * g.nkt : g.nkt) : g.nkt;
+  const int ktot = is_corr ? (g.ncorr == 1 ? 2 * g.nkt : g.nkt) : g.nkt;
+  const int klen = (ktot + g.ksplit - 1) / g.ksplit;
+  const int kbeg = split * klen;
+  // This group's k-steps; 0 for a trailing split past the end (it stores zeros).
+  const int nk = max(0, min(klen, ktot - kbeg));
+  const int kt0 = ((is_corr && g.ncorr == 2) ? slot * g.nkt : 0) + kbeg;
 
   const int8_t* At = g.A + b * g.memberA + (int64_t)plane * g.planeA +
                      ((int64_t)mt * rstride + kt0) * kTileBytes;
@@ -829,8 +877,9 @@ modgemm_kernel(GemmArgs g) {
     // an accumulator tile at the split).
     const int t = is_corr ? 0 : plane;
     const double pd = (double)g.p[t], ip = g.invp[t];
-    int32_t* cdst = g.corr + (b * g.ncorr + (is_corr ? slot : 0)) * g.outplane;
-    int8_t* rdst = g.res8 + (b * g.P + t) * g.outplane;
+    const int64_t sbm = (int64_t)split * g.batch + b;   // split-major output planes
+    int32_t* cdst = g.corr + (sbm * g.ncorr + (is_corr ? slot : 0)) * g.outplane;
+    int8_t* rdst = g.res8 + (sbm * g.P + t) * g.outplane;
 #pragma unroll
     for (int x = 0; x < 4; ++x)
 #pragma unroll
@@ -916,6 +965,7 @@ struct ReconArgs {
   int64_t MBv, NBv;    // 32-blocks covering the valid M, N
   int64_t nblocks;     // batch * MBv * NBv
   int ncorr;
+  int ksplit;            // S: residue / correction planes per output, summed here
   ModTables tab;
 };
 
@@ -961,12 +1011,56 @@ reconstruct_kernel(ReconArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) cv[e] = c[e];
     }
-  } else {
+  } else if (a.ksplit == 1) {
 #pragma unroll
     for (int t = 0; t < kMaxP; ++t)
       if (t < P) w[t] = *reinterpret_cast<const uint32_t*>(a.res8 + (b * P + t) * a.outplane + boff);
+  } else {
+    // K-split: the S partial residues sum (|sum| <= 128 S) and fold to the
+    // residue (any representative serves: each digit reduces mod p again).
+    // Split-outer, plane-inner: the P loads of one split are independent.
+    int sums[kMaxP][4];
+#pragma unroll
+    for (int t = 0; t < kMaxP; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sums[t][e] = 0;
+    for (int sp = 0; sp < a.ksplit; ++sp) {
+      uint32_t u[kMaxP];
+#pragma unroll
+      for (int t = 0; t < kMaxP; ++t)
+        if (t < P)
+          u[t] = *reinterpret_cast<const uint32_t*>(
+              a.res8 + ((sp * a.batch + b) * P + t) * a.outplane + boff);
+#pragma unroll
+      for (int t = 0; t < kMaxP; ++t)
+        if (t < P) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sums[t][e] += (int)(int8_t)(uint8_t)(u[t] >> (8 * e));
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < kMaxP; ++t)
+      if (t < P) {
+        const int* sum4 = sums[t];
+        const double pd = (double)a.tab.p[t], ip = a.tab.invp[t];
+        uint32_t u = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const double vd = (double)sum4[e];
+          u |= ((uint32_t)(int)fma(-floor(fma(vd, ip, kHalfUp)), pd, vd) & 0xFFu) << (8 * e);
+        }
+        w[t] = u;
+      }
   }
-  if (!kDeep && a.ncorr > 0) {
+  if (!kDeep && a.ncorr > 0 && a.ksplit > 1) {
+    for (int sp = 0; sp < a.ksplit; ++sp)
+      for (int cc = 0; cc < a.ncorr; ++cc) {
+        const v4i c1 = *reinterpret_cast<const v4i*>(
+            a.corr + ((sp * a.batch + b) * a.ncorr + cc) * a.outplane + boff);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cv[e] += c1[e];
+      }
+  } else if (!kDeep && a.ncorr > 0) {
     const v4i c1 = *reinterpret_cast<const v4i*>(a.corr + (b * a.ncorr) * a.outplane + boff);
 #pragma unroll
     for (int e = 0; e < 4; ++e) cv[e] = c1[e];
@@ -1271,8 +1365,9 @@ int run(const Call& c) {
   ga.outplane = L.outplane_bytes;
   ga.TM = (int)(L.Mp / kTileR); ga.TN = (int)(L.Np / kTileR);
   ga.P = c.P; ga.ncorr = L.ncorr; ga.nslots = c.P + L.ncorr; ga.batch = (int)c.batch;
+  ga.ksplit = L.ksplit;
   for (int t = 0; t < kMaxP; ++t) { ga.p[t] = tab.p[t]; ga.invp[t] = tab.invp[t]; }
-  ga.total = (int64_t)ga.nslots * c.batch * ga.TM * ga.TN;
+  ga.total = (int64_t)ga.nslots * c.batch * L.ksplit * ga.TM * ga.TN;
   for (int seg = 0; seg < L.nseg; ++seg) {
     const int64_t k0 = (int64_t)seg * L.kseg;
     const int64_t kc = std::min<int64_t>(L.kseg, c.K - k0);
@@ -1321,6 +1416,7 @@ int run(const Call& c) {
     ra.MBv = (c.M + 31) / 32; ra.NBv = (c.N + 31) / 32;
     ra.nblocks = c.batch * ra.MBv * ra.NBv;
     ra.ncorr = L.ncorr;
+    ra.ksplit = L.ksplit;
     ra.tab = tab;
     const unsigned grid = (unsigned)ra.nblocks;
     if (L.deep) {

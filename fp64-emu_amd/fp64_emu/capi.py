@@ -29,7 +29,8 @@ class Layout(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int64), ("M", ctypes.c_int64), ("N", ctypes.c_int64),
                 ("K", ctypes.c_int64), ("nprimes", ctypes.c_int), ("use_corr", ctypes.c_int),
                 ("ncorr", ctypes.c_int), ("nslab", ctypes.c_int), ("deep", ctypes.c_int),
-                ("nseg", ctypes.c_int), ("kseg", ctypes.c_int64), ("Mp", ctypes.c_int64),
+                ("nseg", ctypes.c_int), ("kseg", ctypes.c_int64), ("ksplit", ctypes.c_int),
+                ("reserved", ctypes.c_int), ("Mp", ctypes.c_int64),
                 ("Np", ctypes.c_int64), ("Kp", ctypes.c_int64), ("planeA_bytes", ctypes.c_int64),
                 ("planeB_bytes", ctypes.c_int64), ("memberA_bytes", ctypes.c_int64),
                 ("memberB_bytes", ctypes.c_int64), ("outplane_bytes", ctypes.c_int64)] + [
@@ -286,17 +287,30 @@ def _blocks_to_logical(arr, Mp, Np):
     return a.transpose(0, 4, 2, 5, 1, 3).reshape(Mp, Np)
 
 
-def outputs(ws, lay):
-    """(res8 [batch, P, M, N] int8, corr [batch, ncorr, M, N] int32)."""
+def outputs(ws, lay, primes=None):
+    """(res8 [batch, P, M, N] int8, corr [batch, ncorr, M, N] int64).  With a
+    K-split the S partial residues are summed and reduced to the balanced
+    residue (bal8's convention: r > p/2 -> r - p, as int8), which needs the
+    moduli, and the S partial correction sums are added."""
     w = _ws_bytes(ws)
-    P, Mp, Np, ob = lay.nprimes, lay.Mp, lay.Np, lay.outplane_bytes
+    P, Mp, Np, ob, S = lay.nprimes, lay.Mp, lay.Np, lay.outplane_bytes, max(lay.ksplit, 1)
     res = np.zeros((lay.batch, P, lay.M, lay.N), dtype=np.int8)
-    corr = np.zeros((lay.batch, lay.ncorr, lay.M, lay.N), dtype=np.int32)
+    corr = np.zeros((lay.batch, lay.ncorr, lay.M, lay.N), dtype=np.int64)
+    if S > 1 and primes is None:
+        raise ValueError("a K-split call needs the moduli to fold its residues")
     for b in range(lay.batch):
         for t in range(P):
-            s = lay.off_res8 + (b * P + t) * ob
-            res[b, t] = _blocks_to_logical(w[s:s + ob].view(np.int8), Mp, Np)[:lay.M, :lay.N]
+            acc = np.zeros((lay.M, lay.N), dtype=np.int64)
+            for sp in range(S):
+                s0 = lay.off_res8 + ((sp * lay.batch + b) * P + t) * ob
+                acc += _blocks_to_logical(w[s0:s0 + ob].view(np.int8), Mp, Np)[:lay.M, :lay.N]
+            if S > 1:
+                p = int(primes[t])
+                r = np.mod(acc, p)
+                acc = np.where(r > p // 2, r - p, r)
+            res[b, t] = acc.astype(np.int8)
         for c in range(lay.ncorr):
-            s = lay.off_corr + 4 * (b * lay.ncorr + c) * ob
-            corr[b, c] = _blocks_to_logical(w[s:s + 4 * ob].view(np.int32), Mp, Np)[:lay.M, :lay.N]
+            for sp in range(S):
+                s0 = lay.off_corr + 4 * ((sp * lay.batch + b) * lay.ncorr + c) * ob
+                corr[b, c] += _blocks_to_logical(w[s0:s0 + 4 * ob].view(np.int32), Mp, Np)[:lay.M, :lay.N]
     return res, corr

@@ -123,15 +123,20 @@ typedef struct {
   int deep;                 /* K > 131071: the K-segmented form (mm / bmm only) */
   int nseg;                 /* K segments (1 unless deep) */
   int64_t kseg;             /* depth of one segment (K unless deep: 65536) */
+  int ksplit;               /* GEMM K-split S: S groups per output tile, each over a K
+                               range, with S residue / correction planes summed at
+                               reconstruction (1 unless the tiles are few) */
+  int reserved;
   int64_t Mp, Np, Kp;       /* padded to the 256-row tile and the 64-deep k tile (of one
                                segment when deep) */
   int64_t planeA_bytes;     /* one residue plane of A for one member: Mp*Kp */
   int64_t planeB_bytes;     /* Np*Kp; the correction plane is twice as deep (2*Kp) */
   int64_t memberA_bytes;    /* all planes of one member: (nprimes + 2*use_corr) * Mp*Kp */
   int64_t memberB_bytes;
-  int64_t outplane_bytes;   /* elements of one output plane: Mp*Np.  res8 holds P int8
-                               planes per member (deep: int32 residue sums); corr holds
-                               ncorr int32 planes (deep: one int64 sum plane) */
+  int64_t outplane_bytes;   /* elements of one output plane: Mp*Np.  res8 holds
+                               ksplit x batch x P int8 planes, split-major (deep: int32
+                               residue sums); corr holds ksplit x batch x ncorr int32
+                               planes (deep: one int64 sum plane) */
   size_t off_sftA, off_sftB, off_lgA, off_lgB, off_bits, off_pmax, off_pss;
   size_t off_planesA, off_planesB, off_res8, off_corr, total;
 } fp64emu_layout_t;

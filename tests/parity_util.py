@@ -88,7 +88,7 @@ def check_call(kind, A, B, primes, exact=True, bits=53, use_corr=True, full_orac
         assert np.array_equal(ghB, ohB) and np.array_equal(gqB, oqB), "B hi7/q7 differ"
 
     # GEMM outputs
-    gres8, gcorr = capi.outputs(wsh, lay)
+    gres8, gcorr = capi.outputs(wsh, lay, primes)
     for b in range(batch):
         for t in range(P):
             o8 = O.modgemm(oresA[b, t], oresB[b, t], int(primes[t]))

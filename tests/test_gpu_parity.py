@@ -26,6 +26,7 @@ CASES = [
     ("bmm_nt", 3, 100, 77, 333, 14, True),
     ("bmm", 5, 96, 64, 256, 14, True),
     ("mm", 1, 64, 48, 64, 20, True),
+    ("mm_nt", 1, 64, 40, 100_000, 15, True),    # two int32 correction planes, K-split 16
 ]
 
 
