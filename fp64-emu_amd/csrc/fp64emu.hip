@@ -1320,6 +1320,18 @@ int run(const Call& c) {
   }
   if (!c.A || !c.B) return fail(FP64EMU_EINVAL, "null operand pointer");
   if (!c.ws || c.ws_bytes < L.total) return fail(FP64EMU_EWORKSPACE, "workspace too small");
+  {
+    // A dispatch holds its grid size in work-items as 32 bits.
+    const int64_t limit = (int64_t)0xFFFFFFFFu / kThreads;
+    const int64_t nkt_max = L.Kp / kTileK;
+    const int64_t grids[4] = {
+        MF + NF,                                                   // row sizing
+        c.batch * (L.Mp / 64 + L.Np / 64) * nkt_max,               // extraction
+        (int64_t)(c.P + L.ncorr) * c.batch * L.ksplit * (L.Mp / kTileR) * (L.Np / kTileR),
+        c.batch * ((c.M + 31) / 32) * ((c.N + 31) / 32)};          // reconstruction
+    for (int64_t gsz : grids)
+      if (gsz > limit) return fail(FP64EMU_EINVAL, "problem too large for one launch");
+  }
   const ModTables tab = make_tables(c.primes, c.P);
 
   char* ws = static_cast<char*>(c.ws);
