@@ -168,8 +168,10 @@ def main():
     del Cn
 
     cpu = None
+    cpu_torch = None
     if not args.no_cpu:
         cpu = cpu_baseline(A, Bt, P, corr)
+        cpu_torch = cpu_torch_baseline(A, Bt)
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "modgemm_c2_traffic.json")
@@ -207,6 +209,7 @@ def main():
         "speedup_vs_native": round(value / nat_tf, 3),
         **acc,
         "cpu_baseline": cpu,
+        "cpu_torch_f64": cpu_torch,
     }
     print(json.dumps(rec), flush=True)
 
@@ -315,6 +318,35 @@ def run_configs(steps, warmup):
         torch.cuda.empty_cache()
 
 
+def _host_cores():
+    try:
+        import psutil
+        cores = len(psutil.Process().cpu_affinity())
+    except Exception:
+        cores = os.cpu_count() or 1
+    return max(1, min(cores, 16))
+
+
+def cpu_torch_baseline(A, Bt):
+    """torch float64 matmul of the same workload on the host's cores (the
+    comparison the reference's benchmarks quote beside native DGEMM)."""
+    import torch
+    cores = _host_cores()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    a, bt = A.cpu(), Bt.cpu()
+    torch.matmul(a[:1024], bt[:, :1024])            # warm-up
+    t0 = time.perf_counter()
+    torch.matmul(a, bt)
+    t = time.perf_counter() - t0
+    torch.set_num_threads(prev)
+    n = a.shape[0]
+    val = 2.0 * n * bt.shape[1] * a.shape[1] / t / 1e12
+    log(f"cpu torch float64 matmul ({cores} threads): {t:.2f} s, {val:.4f} TFLOP/s")
+    return {"value": round(val, 5), "unit": "TFLOP/s", "cores": cores, "seconds": round(t, 3),
+            "sample": "the full workload, torch.matmul float64 on host tensors"}
+
+
 def cpu_baseline(A, Bt, P, corr):
     """The oracle port (the reference pipeline restated in C) on the host's
     cores, on a bounded sample of the workload: the first 2048 rows of A and
@@ -322,12 +354,7 @@ def cpu_baseline(A, Bt, P, corr):
     Effective FP64 TFLOPS of that sample (2 * 2048 * 2048 * K / t)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
-    try:
-        import psutil
-        cores = len(psutil.Process().cpu_affinity())
-    except Exception:
-        cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
+    cores = _host_cores()
     m = 2048
     a = A[:m].cpu().numpy()
     bt = Bt[:, :m].contiguous().cpu().numpy()
