@@ -162,8 +162,10 @@ int choose_ksplit(int64_t batch, int64_t tiles, int64_t nkt, int P, int ncorr) {
   return best;
 }
 
+// nchunk_req > 1 (batch 1, not K-segmented): the planes of A and the output
+// planes hold one chunk of ceil(TM / nchunk_req) row tiles at a time.
 void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool corr,
-                 fp64emu_layout_t* L) {
+                 fp64emu_layout_t* L, int64_t nchunk_req = 1) {
   std::memset(L, 0, sizeof(*L));
   L->batch = batch; L->M = M; L->N = N; L->K = K;
   L->nprimes = P; L->use_corr = corr ? 1 : 0;
@@ -180,14 +182,19 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   L->Mp = round_up(std::max<int64_t>(M, 1), kTileR);
   L->Np = round_up(std::max<int64_t>(N, 1), kTileR);
   L->Kp = round_up(L->kseg, kTileK);
-  L->planeA_bytes = L->Mp * L->Kp;
+  const int64_t TM = L->Mp / kTileR;
+  int64_t ctiles = TM;
+  if (nchunk_req > 1 && batch == 1 && !L->deep) ctiles = (TM + nchunk_req - 1) / nchunk_req;
+  L->nchunk = (int)((TM + ctiles - 1) / ctiles);
+  L->chunk_rows = ctiles * kTileR;
+  L->planeA_bytes = L->chunk_rows * L->Kp;
   L->planeB_bytes = L->Np * L->Kp;
   const int nplanes = P + (corr ? 2 : 0);   // the correction plane is 2*Kp deep
   L->memberA_bytes = (int64_t)nplanes * L->planeA_bytes;
   L->memberB_bytes = (int64_t)nplanes * L->planeB_bytes;
-  L->outplane_bytes = L->Mp * L->Np;
-  L->ksplit = L->deep ? 1 : choose_ksplit(batch, (L->Mp / kTileR) * (L->Np / kTileR),
-                                          L->Kp / kTileK, P, L->ncorr);
+  L->outplane_bytes = L->chunk_rows * L->Np;
+  L->ksplit = L->deep ? 1 : choose_ksplit(batch, ctiles * (L->Np / kTileR), L->Kp / kTileK, P,
+                                          L->ncorr);
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o = align_up(o + bytes); return at; };
   L->off_sftA = take(sizeof(int16_t) * batch * M);
@@ -1319,15 +1326,33 @@ int run(const Call& c) {
     return FP64EMU_OK;
   }
   if (!c.A || !c.B) return fail(FP64EMU_EINVAL, "null operand pointer");
-  if (!c.ws || c.ws_bytes < L.total) return fail(FP64EMU_EWORKSPACE, "workspace too small");
+  if (!c.ws) return fail(FP64EMU_EWORKSPACE, "workspace too small");
+  if (c.ws_bytes < L.total) {
+    // Short workspace: the fewest row chunks of A that fit (batch 1, not
+    // K-segmented, no phase events).
+    bool fits = false;
+    if (c.batch == 1 && !L.deep && !c.ev) {
+      const int64_t TM = L.Mp / kTileR;
+      int64_t last_tiles = TM;
+      for (int64_t nc = 2; nc <= TM && !fits; ++nc) {
+        const int64_t ct = (TM + nc - 1) / nc;
+        if (ct == last_tiles) continue;
+        last_tiles = ct;
+        fp64emu_layout_t Lc;
+        make_layout(c.batch, c.M, c.N, c.K, c.P, c.corr, &Lc, nc);
+        if (c.ws_bytes >= Lc.total) { L = Lc; fits = true; }
+      }
+    }
+    if (!fits) return fail(FP64EMU_EWORKSPACE, "workspace too small");
+  }
   {
     // A dispatch holds its grid size in work-items as 32 bits.
     const int64_t limit = (int64_t)0xFFFFFFFFu / kThreads;
     const int64_t nkt_max = L.Kp / kTileK;
     const int64_t grids[4] = {
         MF + NF,                                                   // row sizing
-        c.batch * (L.Mp / 64 + L.Np / 64) * nkt_max,               // extraction
-        (int64_t)(c.P + L.ncorr) * c.batch * L.ksplit * (L.Mp / kTileR) * (L.Np / kTileR),
+        c.batch * (L.chunk_rows / 64 + L.Np / 64) * nkt_max,       // extraction
+        (int64_t)(c.P + L.ncorr) * c.batch * L.ksplit * (L.chunk_rows / kTileR) * (L.Np / kTileR),
         c.batch * ((c.M + 31) / 32) * ((c.N + 31) / 32)};          // reconstruction
     for (int64_t gsz : grids)
       if (gsz > limit) return fail(FP64EMU_EINVAL, "problem too large for one launch");
@@ -1366,8 +1391,10 @@ int run(const Call& c) {
   hipLaunchKernelGGL(pick_width_kernel, dim3(1), dim3(kPickThreads), 0, s, lgA, MF, lgB, NF,
                      std::min(tab.log2M, 126.0f), c.bits, sftA, sftB, bits_eff);
 
-  // 2-3. Per K segment (one unless deep): extraction (covers the padded
-  // planes entirely: no memset needed), then every modular GEMM in one launch.
+  // 2-4. Per row chunk of A (one unless the workspace is short) and per K
+  // segment (one unless deep): extraction (covering the padded planes
+  // entirely, so no memset), every modular GEMM in one launch, then the
+  // reconstruction of the chunk's rows.  B's planes are extracted once.
   GemmArgs ga;
   ga.A = planesA; ga.B = planesB; ga.res8 = res8; ga.corr = corr;
   ga.racc = L.deep ? reinterpret_cast<int32_t*>(res8) : nullptr;
@@ -1375,57 +1402,59 @@ int run(const Call& c) {
   ga.memberA = L.memberA_bytes; ga.memberB = L.memberB_bytes;
   ga.planeA = L.planeA_bytes; ga.planeB = L.planeB_bytes;
   ga.outplane = L.outplane_bytes;
-  ga.TM = (int)(L.Mp / kTileR); ga.TN = (int)(L.Np / kTileR);
+  ga.TM = (int)(L.chunk_rows / kTileR); ga.TN = (int)(L.Np / kTileR);
   ga.P = c.P; ga.ncorr = L.ncorr; ga.nslots = c.P + L.ncorr; ga.batch = (int)c.batch;
   ga.ksplit = L.ksplit;
   for (int t = 0; t < kMaxP; ++t) { ga.p[t] = tab.p[t]; ga.invp[t] = tab.invp[t]; }
   ga.total = (int64_t)ga.nslots * c.batch * L.ksplit * ga.TM * ga.TN;
-  for (int seg = 0; seg < L.nseg; ++seg) {
-    const int64_t k0 = (int64_t)seg * L.kseg;
-    const int64_t kc = std::min<int64_t>(L.kseg, c.K - k0);
-    const int64_t nkt = round_up(kc, kTileK) / kTileK;
-    ExtractArgs ea;
-    ea.A = c.A; ea.B = c.B;
-    ea.M = c.M; ea.N = c.N; ea.K = kc; ea.batch = c.batch;
-    ea.lda = c.K; ea.k0 = k0;
-    ea.b_kn = c.b_kn ? 1 : 0;
-    ea.use_corr = c.corr ? 1 : 0;
-    ea.nkt = nkt;
-    ea.planeA = L.planeA_bytes; ea.planeB = L.planeB_bytes;
-    ea.memberA = L.memberA_bytes; ea.memberB = L.memberB_bytes;
-    ea.rgA = L.Mp / 64; ea.rgB = L.Np / 64;
-    ea.wgA = c.batch * ea.rgA * nkt;
-    ea.sftA = sftA; ea.sftB = sftB; ea.bits_eff = bits_eff;
-    ea.planesA = planesA; ea.planesB = planesB;
-    ea.tab = tab;
-    const int64_t wg = ea.wgA + c.batch * ea.rgB * nkt;
-    hipLaunchKernelGGL(extract_kernel, dim3((unsigned)wg), dim3(kThreads), 0, s, ea);
-    if (c.ev) {
-      if (int st = check_hip(hipEventRecord(c.ev[1], s), "hipEventRecord")) return st;
+  for (int ci = 0; ci < L.nchunk; ++ci) {
+    const int64_t m0 = (int64_t)ci * L.chunk_rows;              // 0 unless chunked (batch 1)
+    const int64_t Mc = std::min<int64_t>(L.chunk_rows, c.M - m0);
+    const bool with_B = L.nchunk == 1 || ci == 0;
+    for (int seg = 0; seg < L.nseg; ++seg) {
+      const int64_t k0 = (int64_t)seg * L.kseg;
+      const int64_t kc = std::min<int64_t>(L.kseg, c.K - k0);
+      const int64_t nkt = round_up(kc, kTileK) / kTileK;
+      ExtractArgs ea;
+      ea.A = c.A + m0 * c.K; ea.B = c.B;
+      ea.M = Mc; ea.N = c.N; ea.K = kc; ea.batch = c.batch;
+      ea.lda = c.K; ea.k0 = k0;
+      ea.b_kn = c.b_kn ? 1 : 0;
+      ea.use_corr = c.corr ? 1 : 0;
+      ea.nkt = nkt;
+      ea.planeA = L.planeA_bytes; ea.planeB = L.planeB_bytes;
+      ea.memberA = L.memberA_bytes; ea.memberB = L.memberB_bytes;
+      ea.rgA = L.chunk_rows / 64; ea.rgB = with_B ? L.Np / 64 : 0;
+      ea.wgA = c.batch * ea.rgA * nkt;
+      ea.sftA = sftA + m0; ea.sftB = sftB; ea.bits_eff = bits_eff;
+      ea.planesA = planesA; ea.planesB = planesB;
+      ea.tab = tab;
+      const int64_t wg = ea.wgA + c.batch * ea.rgB * nkt;
+      hipLaunchKernelGGL(extract_kernel, dim3((unsigned)wg), dim3(kThreads), 0, s, ea);
+      if (c.ev) {
+        if (int st = check_hip(hipEventRecord(c.ev[1], s), "hipEventRecord")) return st;
+      }
+      ga.nkt = (int)nkt;
+      ga.first = seg == 0 ? 1 : 0;
+      if (L.deep)
+        hipLaunchKernelGGL(modgemm_kernel<true>, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+      else
+        hipLaunchKernelGGL(modgemm_kernel<false>, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
     }
-    ga.nkt = (int)nkt;
-    ga.first = seg == 0 ? 1 : 0;
-    if (L.deep)
-      hipLaunchKernelGGL(modgemm_kernel<true>, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
-    else
-      hipLaunchKernelGGL(modgemm_kernel<false>, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
-  }
-  if (c.ev) {
-    if (int st = check_hip(hipEventRecord(c.ev[2], s), "hipEventRecord")) return st;
-    if (int st = check_hip(hipEventRecord(c.ev[3], s), "hipEventRecord")) return st;
-  }
+    if (c.ev) {
+      if (int st = check_hip(hipEventRecord(c.ev[2], s), "hipEventRecord")) return st;
+      if (int st = check_hip(hipEventRecord(c.ev[3], s), "hipEventRecord")) return st;
+    }
 
-  // 4. reconstruction
-  {
     ReconArgs ra;
     ra.res8 = res8; ra.corr = corr;
     ra.res32 = reinterpret_cast<const int32_t*>(res8);
     ra.corr64 = reinterpret_cast<const int64_t*>(corr);
-    ra.out = c.out;
-    ra.sftA = sftA; ra.sftB = sftB; ra.bits_eff = bits_eff;
-    ra.M = c.M; ra.N = c.N; ra.batch = c.batch; ra.outplane = L.outplane_bytes;
+    ra.out = c.out + m0 * c.N;
+    ra.sftA = sftA + m0; ra.sftB = sftB; ra.bits_eff = bits_eff;
+    ra.M = Mc; ra.N = c.N; ra.batch = c.batch; ra.outplane = L.outplane_bytes;
     ra.NB = L.Np / 32;
-    ra.MBv = (c.M + 31) / 32; ra.NBv = (c.N + 31) / 32;
+    ra.MBv = (Mc + 31) / 32; ra.NBv = (c.N + 31) / 32;
     ra.nblocks = c.batch * ra.MBv * ra.NBv;
     ra.ncorr = L.ncorr;
     ra.ksplit = L.ksplit;
@@ -1480,6 +1509,14 @@ size_t fp64emu_workspace_size(int64_t batch, int64_t M, int64_t N, int64_t K, in
   if (batch < 0 || M < 0 || N < 0 || K < 0 || nprimes < 1 || nprimes > kMaxP) return 0;
   fp64emu_layout_t L;
   make_layout(batch, M, N, K, nprimes, use_corr != 0, &L);
+  return L.total;
+}
+
+size_t fp64emu_workspace_size_min(int64_t batch, int64_t M, int64_t N, int64_t K, int nprimes,
+                                  int use_corr) {
+  if (batch < 0 || M < 0 || N < 0 || K < 0 || nprimes < 1 || nprimes > kMaxP) return 0;
+  fp64emu_layout_t L;
+  make_layout(batch, M, N, K, nprimes, use_corr != 0, &L, round_up(std::max<int64_t>(M, 1), kTileR) / kTileR);
   return L.total;
 }
 

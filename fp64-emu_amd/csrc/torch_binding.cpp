@@ -31,6 +31,22 @@ at::Tensor workspace(const at::Tensor& like, size_t bytes) {
   return at::empty({(int64_t)std::max<size_t>(bytes, 1)}, like.options().dtype(at::kByte));
 }
 
+// The full workspace when the caching allocator can provide it; otherwise
+// the largest of full/2, full/4, ... down to the minimum the library accepts
+// (it then runs the rows of A in as few chunks as fit).  Only batch-1 calls
+// with K <= 131071 have a smaller minimum; the others need the full size.
+at::Tensor workspace_fit(const at::Tensor& like, size_t full, size_t minimum) {
+  size_t want = full;
+  while (want > minimum) {
+    try {
+      return workspace(like, want);
+    } catch (const c10::OutOfMemoryError&) {
+      want /= 2;
+    }
+  }
+  return workspace(like, minimum);
+}
+
 fp64emu_stream_t current_stream(const at::Tensor& t) {
   return reinterpret_cast<fp64emu_stream_t>(
       c10::hip::getCurrentHIPStream(t.device().index()).stream());
@@ -73,7 +89,8 @@ void fp64_emu_mm(at::Tensor& out, const at::Tensor& A, const at::Tensor& B,
   const c10::DeviceGuard guard(A.device());
   const std::vector<int32_t> pv = primes_vec(primes_cpu);
   const int P = (int)pv.size();
-  at::Tensor ws = workspace(A, fp64emu_workspace_size(1, M, N, K, P, use_corr));
+  at::Tensor ws = workspace_fit(A, fp64emu_workspace_size(1, M, N, K, P, use_corr),
+                                fp64emu_workspace_size_min(1, M, N, K, P, use_corr));
   check_status(fp64emu_mm(out.data_ptr<double>(), A.data_ptr<double>(), B.data_ptr<double>(), M,
                           N, K, pv.data(), nullptr, nullptr, P, exact, bits, use_corr,
                           ws.data_ptr(), (size_t)ws.numel(), current_stream(A)));
@@ -95,7 +112,8 @@ void fp64_emu_mm_nt(at::Tensor& out, const at::Tensor& A, const at::Tensor& Bt,
   const c10::DeviceGuard guard(A.device());
   const std::vector<int32_t> pv = primes_vec(primes_cpu);
   const int P = (int)pv.size();
-  at::Tensor ws = workspace(A, fp64emu_workspace_size(1, M, N, K, P, use_corr));
+  at::Tensor ws = workspace_fit(A, fp64emu_workspace_size(1, M, N, K, P, use_corr),
+                                fp64emu_workspace_size_min(1, M, N, K, P, use_corr));
   check_status(fp64emu_mm_nt(out.data_ptr<double>(), A.data_ptr<double>(), Bt.data_ptr<double>(),
                              M, N, K, pv.data(), nullptr, nullptr, P, exact, bits, use_corr,
                              ws.data_ptr(), (size_t)ws.numel(), current_stream(A)));

@@ -20,7 +20,8 @@ CAPI_PATH = os.path.join(_HERE, "libfp64emu.so")
 TILE_R, TILE_K, FRAG = 256, 64, 1024
 
 # Every function declared in include/fp64emu.h.
-EXPORTS = ("fp64emu_maxp", "fp64emu_last_error", "fp64emu_workspace_size", "fp64emu_mm",
+EXPORTS = ("fp64emu_maxp", "fp64emu_last_error", "fp64emu_workspace_size",
+           "fp64emu_workspace_size_min", "fp64emu_mm",
            "fp64emu_mm_nt", "fp64emu_bmm", "fp64emu_bmm_nt", "fp64emu_mm_timed",
            "fp64emu_mm_nt_events", "fp64emu_layout", "fp64emu_ddgemm_nt")
 
@@ -30,7 +31,7 @@ class Layout(ctypes.Structure):
                 ("K", ctypes.c_int64), ("nprimes", ctypes.c_int), ("use_corr", ctypes.c_int),
                 ("ncorr", ctypes.c_int), ("nslab", ctypes.c_int), ("deep", ctypes.c_int),
                 ("nseg", ctypes.c_int), ("kseg", ctypes.c_int64), ("ksplit", ctypes.c_int),
-                ("reserved", ctypes.c_int), ("Mp", ctypes.c_int64),
+                ("nchunk", ctypes.c_int), ("chunk_rows", ctypes.c_int64), ("Mp", ctypes.c_int64),
                 ("Np", ctypes.c_int64), ("Kp", ctypes.c_int64), ("planeA_bytes", ctypes.c_int64),
                 ("planeB_bytes", ctypes.c_int64), ("memberA_bytes", ctypes.c_int64),
                 ("memberB_bytes", ctypes.c_int64), ("outplane_bytes", ctypes.c_int64)] + [
@@ -55,6 +56,8 @@ def lib():
     L.fp64emu_last_error.restype = ctypes.c_char_p
     L.fp64emu_workspace_size.argtypes = [i64, i64, i64, i64, i32, i32]
     L.fp64emu_workspace_size.restype = sz
+    L.fp64emu_workspace_size_min.argtypes = [i64, i64, i64, i64, i32, i32]
+    L.fp64emu_workspace_size_min.restype = sz
     mm_args = [vp, vp, vp, i64, i64, i64, vp, vp, vp, i32, i32, i64, i32, vp, sz, vp]
     for name in ("fp64emu_mm", "fp64emu_mm_nt"):
         getattr(L, name).argtypes = mm_args
@@ -93,6 +96,10 @@ def layout(batch, M, N, K, nprimes, use_corr):
 
 def workspace_size(batch, M, N, K, nprimes, use_corr):
     return lib().fp64emu_workspace_size(batch, M, N, K, nprimes, int(bool(use_corr)))
+
+
+def workspace_size_min(batch, M, N, K, nprimes, use_corr):
+    return lib().fp64emu_workspace_size_min(batch, M, N, K, nprimes, int(bool(use_corr)))
 
 
 def _stream():

@@ -64,6 +64,16 @@ const char* fp64emu_last_error(void);
 size_t fp64emu_workspace_size(int64_t batch, int64_t M, int64_t N, int64_t K,
                               int nprimes, int use_corr);
 
+/* The smallest workspace a call accepts.  With less than
+ * fp64emu_workspace_size() bytes, a call with batch 1 and K <= 131071 runs
+ * the rows of A in chunks of 256-row multiples against one extraction of B
+ * (the fewest chunks that fit), so products too large for the full
+ * workspace still run.  Other calls need the full size.  No reference
+ * counterpart: the reference allocates its scratch per call (README.md:105-107
+ * describes chunking only for its cuBLAS engine). */
+size_t fp64emu_workspace_size_min(int64_t batch, int64_t M, int64_t N, int64_t K,
+                                  int nprimes, int use_corr);
+
 /* out[M,N] = A[M,K] @ B[N,K]^T; K up to 128 * 65536, K-segmented past 131071
  * (fp64_emu_cuda/fp64_emu.cu:1479-1579).   fp64_emu_cuda/fp64_emu.cu:1583-1608 */
 int fp64emu_mm(double* out, const double* A, const double* B, int64_t M, int64_t N, int64_t K,
@@ -126,7 +136,9 @@ typedef struct {
   int ksplit;               /* GEMM K-split S: S groups per output tile, each over a K
                                range, with S residue / correction planes summed at
                                reconstruction (1 unless the tiles are few) */
-  int reserved;
+  int nchunk;               /* row chunks of A (1 unless the workspace is smaller than
+                               fp64emu_workspace_size; batch 1 only) */
+  int64_t chunk_rows;       /* rows of A per chunk (a multiple of 256) */
   int64_t Mp, Np, Kp;       /* padded to the 256-row tile and the 64-deep k tile (of one
                                segment when deep) */
   int64_t planeA_bytes;     /* one residue plane of A for one member: Mp*Kp */

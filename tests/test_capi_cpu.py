@@ -223,3 +223,19 @@ def test_import_fails_loudly_without_extension(tmp_path):
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "not built" in r.stdout
+
+
+@pytest.mark.parametrize("shape", [(1, 1000, 700, 3000), (1, 8192, 8192, 8192), (1, 300, 20, 65537),
+                                   (4, 600, 500, 700), (1, 900, 800, 140000)])
+def test_minimum_workspace(shape):
+    """Batch-1 products with K <= 131071 accept a workspace down to one
+    256-row chunk of A; batched and K-segmented products need the full size."""
+    batch, M, N, K = shape
+    full = capi.workspace_size(batch, M, N, K, 14, True)
+    wmin = capi.workspace_size_min(batch, M, N, K, 14, True)
+    L = capi.layout(batch, M, N, K, 14, True)
+    assert L.nchunk == 1 and L.chunk_rows == L.Mp
+    if batch == 1 and K <= 131071 and L.Mp > 256:
+        assert 0 < wmin < full
+    else:
+        assert wmin == full

@@ -114,3 +114,27 @@ def test_deep_k_parity(dev, kind, batch, M, N, K, P, corr, exact):
     oout, info = O.mm(Ah, Bh, 0, O.PRIMES[:P], exact=exact, use_corr=corr)
     assert info["bits_eff"] == gbe
     assert bits_equal(out.cpu().numpy(), oout), "deep-K output differs from the oracle"
+
+
+@pytest.mark.parametrize("kind,M,N,K", [("mm_nt", 1000, 700, 3000), ("mm", 777, 300, 1500),
+                                        ("mm_nt", 2000, 100, 4096)])
+def test_row_chunks_match_full(dev, kind, M, N, K):
+    """A workspace below the full size runs the rows of A in chunks against
+    one extraction of B; the output is bit-identical to the full run, at
+    the minimum workspace and at one in between."""
+    from fp64_emu import capi
+    print(f"case row-chunks {kind} {M}x{N}x{K}", flush=True)
+    A = _randn((M, K), M + K, dev)
+    B = _randn((K, N) if kind == "mm_nt" else (N, K), N + K, dev)
+    P = 14
+    full, _, _ = capi.run(kind, A, B, O.PRIMES[:P])
+    wfull = capi.workspace_size(1, M, N, K, P, True)
+    wmin = capi.workspace_size_min(1, M, N, K, P, True)
+    assert wmin < wfull
+    for wbytes in (wmin, (wmin + wfull) // 2):
+        ws = torch.empty(wbytes, dtype=torch.uint8, device=dev)
+        out, _, _ = capi.run(kind, A, B, O.PRIMES[:P], ws=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(out, full), f"workspace {wbytes}"
+    with pytest.raises(capi.CapiError, match="workspace too small"):
+        capi.run(kind, A, B, O.PRIMES[:P], ws=torch.empty(wmin - 256, dtype=torch.uint8, device=dev))
