@@ -634,6 +634,23 @@ __device__ __forceinline__ int acc_read(int a) {
   return v;
 }
 
+// Balanced residue of one int32 modular-GEMM accumulator: acc - q p with q the
+// nearest integer to acc RN(1/p), read off the low word of
+// fma(acc, RN(1/p), kMagic) (the sum's mantissa holds 2^51 + q).  A group of
+// klen <= 131071 k-terms of balanced residues gives |acc| <= klen p^2/4, so
+// |q| <= klen p/4 + 1 < 2^23 and the 24-bit multiply-add is exact.
+__device__ __forceinline__ int acc_residue(int acc, double ip, int negp) {
+  const int q = __double2loint(fma((double)acc, ip, kMagic));
+  return __mul24(q, negp) + acc;
+}
+
+// Low bytes of four ints, packed little-endian into one dword.
+__device__ __forceinline__ uint32_t pack_bytes(int r0, int r1, int r2, int r3) {
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)r1, (uint32_t)r0, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)r3, (uint32_t)r2, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
 constexpr int kStages = 4;                   // LDS ring: 4 x 32 KiB
 constexpr int kStageBytes = 2 * kTileBytes;  // A tile then B tile
 constexpr int kDmaPerStep = 8;               // per wave: 4 KiB of A + 4 KiB of B
@@ -856,7 +873,8 @@ modgemm_kernel(GemmArgs g) {
   } else if (kDeep) {
     // K-segmented: balanced residues of this segment join the int32 sums.
     const int t = plane;
-    const double pd = (double)g.p[t], ip = g.invp[t];
+    const double ip = g.invp[t];
+    const int negp = -g.p[t];
     int32_t* dst = g.racc + (b * g.P + t) * g.outplane;
 #pragma unroll
     for (int x = 0; x < 4; ++x)
@@ -867,12 +885,9 @@ modgemm_kernel(GemmArgs g) {
         for (int q = 0; q < 4; ++q) {
           v4i v;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const double av = (double)acc[x][y][4 * q + u];
-            const double qq = fma(av, ip, kMagic) - kMagic;
+          for (int u = 0; u < 4; ++u)
             // +p/2 (p = 256) is -p/2 in the balanced range: the int8 value
-            v[u] = (int)(int8_t)(uint8_t)((uint32_t)(int)fma(-qq, pd, av) & 0xFFu);
-          }
+            v[u] = (int)(int8_t)acc_residue(acc[x][y][4 * q + u], ip, negp);
           if (!g.first) v += d[q];
           d[q] = v;
         }
@@ -883,7 +898,8 @@ modgemm_kernel(GemmArgs g) {
     // keep the same live ranges (two separate loops made the compiler spill
     // an accumulator tile at the split).
     const int t = is_corr ? 0 : plane;
-    const double pd = (double)g.p[t], ip = g.invp[t];
+    const double ip = g.invp[t];
+    const int negp = -g.p[t];
     const int64_t sbm = (int64_t)split * g.batch + b;   // split-major output planes
     int32_t* cdst = g.corr + (sbm * g.ncorr + (is_corr ? slot : 0)) * g.outplane;
     int8_t* rdst = g.res8 + (sbm * g.P + t) * g.outplane;
@@ -902,16 +918,10 @@ modgemm_kernel(GemmArgs g) {
           uint32_t w[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            uint32_t u = 0u;
+            int r[4];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              // |acc| < 2^31: the nearest quotient is exact (see extraction).
-              const double av = (double)acc_read(acc[x][y][4 * q + v]);
-              const double qq = fma(av, ip, kMagic) - kMagic;
-              const int rr = (int)fma(-qq, pd, av);
-              u |= ((uint32_t)rr & 0xFFu) << (8 * v);
-            }
-            w[q] = u;
+            for (int v = 0; v < 4; ++v) r[v] = acc_residue(acc_read(acc[x][y][4 * q + v]), ip, negp);
+            w[q] = pack_bytes(r[0], r[1], r[2], r[3]);
           }
           *reinterpret_cast<v4i*>(rdst + blk) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
         }
@@ -1003,15 +1013,10 @@ reconstruct_kernel(ReconArgs a) {
     for (int t = 0; t < kMaxP; ++t)
       if (t < P) {
         const v4i v = *reinterpret_cast<const v4i*>(a.res32 + (b * P + t) * a.outplane + boff);
-        const double pd = (double)a.tab.p[t], ip = a.tab.invp[t];
-        uint32_t u = 0u;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const double vd = (double)v[e];
-          const double qq = fma(vd, ip, kMagic) - kMagic;
-          u |= ((uint32_t)(int)fma(-qq, pd, vd) & 0xFFu) << (8 * e);
-        }
-        w[t] = u;
+        const double ip = a.tab.invp[t];
+        const int negp = -a.tab.p[t];
+        w[t] = pack_bytes(acc_residue(v[0], ip, negp), acc_residue(v[1], ip, negp),
+                          acc_residue(v[2], ip, negp), acc_residue(v[3], ip, negp));
       }
     if (a.ncorr > 0) {
       const int64_t* c = a.corr64 + b * a.outplane + boff;
