@@ -30,6 +30,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <type_traits>
 
 #include "fp64emu.h"
 
@@ -72,7 +73,7 @@ struct ModTables {
   int P;
   int p[kMaxP];
   int minv[kMaxP];                 // (M_t mod p_t)^-1 mod p_t, M_t = prod_{u<t} p_u
-  int mp[kMaxP * kGarnerWords];    // balanced int8 (M_u mod p_t) for u < t, 4 per word
+  int nmp[kMaxP * kGarnerWords];   // balanced int8 (-M_u mod p_t) for u < t, 4 per word
   long long m64[2];                // prod of moduli 0..6 and 7..13 (1 if empty)
   double invp[kMaxP];              // RN(1 / p)
   double c27[kMaxP];               // 2^27 mod p
@@ -113,9 +114,9 @@ ModTables make_tables(const int32_t* primes, int P) {
     l2 += (float)std::log2((double)pt);
     long long Mu = 1 % pt;   // M_u mod p_t, running over u
     for (int u = 0; u < t; ++u) {
-      int bal = (int)Mu;
+      int bal = (int)((pt - Mu) % pt);   // -M_u mod p_t, balanced
       if (bal > (pt - 1) / 2) bal -= pt;
-      T.mp[t * kGarnerWords + (u >> 2)] |= (int)((uint32_t)(uint8_t)(int8_t)bal << (8 * (u & 3)));
+      T.nmp[t * kGarnerWords + (u >> 2)] |= (int)((uint32_t)(uint8_t)(int8_t)bal << (8 * (u & 3)));
       Mu = (Mu * (primes[u] % pt)) % pt;
     }
     T.minv[t] = inv_mod((int)Mu, pt);
@@ -530,8 +531,13 @@ extract_kernel(ExtractArgs a) {
   const int64_t plane = isA ? a.planeA : a.planeB;
   int8_t* base = (isA ? a.planesA : a.planesB) + b * (isA ? a.memberA : a.memberB);
   const int64_t off = (rt * nkt + kt) * kTileBytes + fr * kFragBytes + lane * 16;
-  for (int pi = 0; pi < P; ++pi) {
-    const double pd = (double)a.tab.p[pi], ip = a.tab.invp[pi], c27 = a.tab.c27[pi];
+  // rr = v - p RNE(v/p) lies in [-p/2, p/2]: balanced for odd p, and for
+  // p = 256 the byte of +128 is that of -128.  Another even p turns a tie's
+  // +p/2 into barrett_bal32's -p/2 (a separate copy of the loop, so the
+  // usual moduli carry no extra compare).
+  auto plane_residues = [&](auto tie_fix, int pi) {
+    const int pt = a.tab.p[pi];
+    const double pd = (double)pt, ip = a.tab.invp[pi], c27 = a.tab.c27[pi];
     uint32_t w4[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -540,13 +546,19 @@ extract_kernel(ExtractArgs a) {
       for (int u = 0; u < 4; ++u) {
         const double v = fma(th[4 * g + u], c27, tl[4 * g + u]);
         const double q = fma(v, ip, kMagic) - kMagic;
-        const int rr = (int)fma(-q, pd, v);
+        int rr = (int)fma(-q, pd, v);
+        if (decltype(tie_fix)::value) rr = rr == (pt >> 1) ? -(pt >> 1) : rr;
         w |= ((uint32_t)rr & 0xFFu) << (8 * u);
       }
       w4[g] = w;
     }
     *reinterpret_cast<v4i*>(base + pi * plane + off) =
         v4i{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
+  };
+  for (int pi = 0; pi < P; ++pi) {
+    const int pt = a.tab.p[pi];
+    if ((pt & 1) || pt == 256) plane_residues(std::false_type{}, pi);
+    else plane_residues(std::true_type{}, pi);
   }
   if (a.use_corr) {
     // Correction plane: row tile stride 2*nkt tiles; A = [hi | q], B = [q | hi].
@@ -875,6 +887,9 @@ modgemm_kernel(GemmArgs g) {
     const int t = plane;
     const double ip = g.invp[t];
     const int negp = -g.p[t];
+    // bal8's range [-(p/2 - 1), p/2] for even p (for p = 256 the same bytes).
+    const bool tie_fix = !(g.p[t] & 1) && g.p[t] != 256;
+    const int half_lo = -(g.p[t] >> 1);
     int32_t* dst = g.racc + (b * g.P + t) * g.outplane;
 #pragma unroll
     for (int x = 0; x < 4; ++x)
@@ -885,9 +900,12 @@ modgemm_kernel(GemmArgs g) {
         for (int q = 0; q < 4; ++q) {
           v4i v;
 #pragma unroll
-          for (int u = 0; u < 4; ++u)
+          for (int u = 0; u < 4; ++u) {
+            int r = acc_residue(acc[x][y][4 * q + u], ip, negp);
+            if (tie_fix) r = r == half_lo ? -half_lo : r;
             // +p/2 (p = 256) is -p/2 in the balanced range: the int8 value
-            v[u] = (int)(int8_t)acc_residue(acc[x][y][4 * q + u], ip, negp);
+            v[u] = (int)(int8_t)r;
+          }
           if (!g.first) v += d[q];
           d[q] = v;
         }
@@ -900,6 +918,9 @@ modgemm_kernel(GemmArgs g) {
     const int t = is_corr ? 0 : plane;
     const double ip = g.invp[t];
     const int negp = -g.p[t];
+    // Residues in [-p/2, p/2]: bal8's range for odd p and, bytewise, for
+    // p = 256; another even p has its ties' -p/2 turned into bal8's +p/2 by
+    // tie_fix_kernel after this launch.
     const int64_t sbm = (int64_t)split * g.batch + b;   // split-major output planes
     int32_t* cdst = g.corr + (sbm * g.ncorr + (is_corr ? slot : 0)) * g.outplane;
     int8_t* rdst = g.res8 + (sbm * g.P + t) * g.outplane;
@@ -987,7 +1008,9 @@ struct ReconArgs {
 };
 
 // kP: the modulus count fixed at compile time (0: read from the tables), so
-// the digit loops unroll to exactly P steps without guards.
+// the digit loops unroll to exactly P steps without guards.  kP > 0 also
+// takes the usual moduli order (first odd or 256, the others odd); kP = 0
+// handles any admissible set.
 template <bool kExact, bool kDeep, int kP>
 __global__ void __launch_bounds__(kThreads)
 reconstruct_kernel(ReconArgs a) {
@@ -1004,6 +1027,7 @@ reconstruct_kernel(ReconArgs a) {
   if (j >= a.N || i0 >= a.M) return;
 
   const int P = kP > 0 ? kP : a.tab.P;
+  constexpr bool kUsual = kP > 0;
   const int64_t boff = (mb * a.NB + nb) * 1024 + 4 * thr;  // byte (int8) / element (int32)
   uint32_t w[kMaxP];
   int64_t cv[4] = {0, 0, 0, 0};
@@ -1097,41 +1121,52 @@ reconstruct_kernel(ReconArgs a) {
     const int pt = a.tab.p[t];
     pv[t] = pt;
     if (t == 0) {
-      // M_0 = 1: the first digit is the residue itself, brought into
-      // [-p/2, (p-1)/2] (a no-op for p = 256, whose bytes are that range).
+      // M_0 = 1: the first digit is the residue.  The GEMM epilogue and the
+      // folds above leave it in [-p/2, (p-1)/2] for odd p (nearest quotient)
+      // and for p = 256 (any representative's low byte is that range); any
+      // other even p is brought there by the floor rule of barrett_bal32.
+      const bool norm = !kUsual && !(pt & 1) && pt != 256;
       const double pd0 = (double)pt, ip0 = a.tab.invp[0];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const double rd = (double)(int)(int8_t)(uint8_t)(w[0] >> (8 * e));
-        const int d = (int)fma(-floor(fma(rd, ip0, kHalfUp)), pd0, rd);
+        int d = (int)(int8_t)(uint8_t)(w[0] >> (8 * e));
+        if (norm) {
+          const double rd = (double)d;
+          d = (int)fma(-floor(fma(rd, ip0, kHalfUp)), pd0, rd);
+        }
         dg[e][0] = d;
-        dp[e][0] = (int)((uint32_t)d & 0xFFu);
+        dp[e][0] = d;   // bytes 1..3 meet zero factors until digits 1..3 land there
       }
       continue;
     }
     const int mi = a.tab.minv[t];
-    const double pd = (double)pt, ip = a.tab.invp[t];
-    int mpw[kGarnerWords];
+    const double nip = -a.tab.invp[t];
+    int nmw[kGarnerWords];
 #pragma unroll
-    for (int g = 0; g < kGarnerWords; ++g) mpw[g] = (4 * g < t) ? a.tab.mp[t * kGarnerWords + g] : 0;
+    for (int g = 0; g < kGarnerWords; ++g) nmw[g] = (4 * g < t) ? a.tab.nmp[t * kGarnerWords + g] : 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int rt = (int)(int8_t)(uint8_t)(w[t] >> (8 * e));
-      int acc = 0;                                      // |acc| < 19 * 128 * 128 < 2^19
+      // x = r_t - sum_{u<t} d_u (M_u mod p_t), seeded with r_t (|x| < 2^19).
+      int x = (int)(int8_t)(uint8_t)(w[t] >> (8 * e));
 #pragma unroll
       for (int g = 0; g < kGarnerWords; ++g)
-        if (4 * g < t) acc = __builtin_amdgcn_sdot4(dp[e][g], mpw[g], acc, false);
-      const double yd = (double)__mul24(rt - acc, mi);  // |y| < 2^27, 24-bit operands
-      // d = y - p floor(y/p + 1/2): the offset 2^-20 outweighs the rounding
-      // of y RN(1/p) (< 2^-26) and stays far below the gap 1/p to the next
-      // integer, so d lies in [-p/2, (p-1)/2] for odd and even p alike
-      // (barrett_bal32's range) with no tie fixup.
-      const double qq = floor(fma(yd, ip, kHalfUp));
-      dg[e][t] = (int)fma(-qq, pd, yd);
+        if (4 * g < t) x = __builtin_amdgcn_sdot4(dp[e][g], nmw[g], x, false);
+      const int y = __mul24(x, mi);                       // |y| < 2^27, 24-bit operands
+      // d = y - p q, q the nearest integer to y/p (-q is the low word of the
+      // fma rounding -y/p; |q| < 2^20).  Odd p has no ties: d lies in
+      // [-(p-1)/2, (p-1)/2].  Even p may give +p/2, barrett_bal32's -p/2.
+      int d = __mul24(__double2loint(fma((double)y, nip, kMagic)), pt) + y;
+      if (!kUsual && !(pt & 1)) d = d == (pt >> 1) ? -(pt >> 1) : d;
+      dg[e][t] = d;
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      dp[e][t >> 2] |= (int)(((uint32_t)dg[e][t] & 0xFFu) << (8 * (t & 3)));
+    for (int e = 0; e < 4; ++e) {
+      const int sh = 8 * (t & 3);
+      // Insert the digit's low byte at byte t % 4 of its word.
+      dp[e][t >> 2] = (t & 3) == 0 ? dg[e][t]
+                                   : (int)__builtin_amdgcn_perm((uint32_t)dg[e][t], (uint32_t)dp[e][t >> 2],
+                                                                 (0x03020100u & ~(0xFFu << sh)) | (0x04u << sh));
+    }
   }
 
   // Horner per group of 7 (digits 7g .. 7g+6, high to low): group position
@@ -1181,6 +1216,26 @@ reconstruct_kernel(ReconArgs a) {
       val = acc;
     }
     a.out[(b * a.M + i) * a.N + j] = ldexp(val, sh);
+  }
+}
+
+// bal8's range for an even modulus other than 256 is [-(p/2 - 1), p/2]; the
+// GEMM epilogue's nearest quotient leaves ties at -p/2.  This pass turns
+// those bytes into +p/2 in every residue plane of that modulus (nplanes
+// planes, plane_stride bytes apart).  Default modulus sets never launch it.
+__global__ void __launch_bounds__(kThreads)
+tie_fix_kernel(int8_t* res8, int64_t outplane, int64_t nplanes, int64_t plane_stride, int p) {
+  const int8_t lo = (int8_t)(-(p >> 1)), hi = (int8_t)(p >> 1);
+  const int64_t words = outplane / 16, n = nplanes * words;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads) {
+    const int64_t pl = i / words;
+    v4i* q = reinterpret_cast<v4i*>(res8 + pl * plane_stride) + (i - pl * words);
+    v4i v = *q;
+    int8_t* b = reinterpret_cast<int8_t*>(&v);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) b[e] = b[e] == lo ? hi : b[e];
+    *q = v;
   }
 }
 
@@ -1276,7 +1331,11 @@ int validate_primes(const int32_t* primes, int P) {
 // reconstruction compiled for their exact count; others use the generic one.
 template <bool kExact>
 void launch_reconstruct_p(int P, unsigned grid, hipStream_t s, const ReconArgs& ra) {
-  switch (P) {
+  // The specialised kernels take the first modulus odd or 256 and the others
+  // odd (every prefix of the default set); other sets run the generic one.
+  bool usual = ra.tab.p[0] == 256 || (ra.tab.p[0] & 1);
+  for (int t = 1; t < P; ++t) usual = usual && (ra.tab.p[t] & 1);
+  switch (usual ? P : 0) {
 #define FP64EMU_RECON_CASE(n)                                                                 \
     case n:                                                                                   \
       hipLaunchKernelGGL((reconstruct_kernel<kExact, false, n>), dim3(grid), dim3(kThreads),  \
@@ -1445,6 +1504,14 @@ int run(const Call& c) {
         hipLaunchKernelGGL(modgemm_kernel<true>, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       else
         hipLaunchKernelGGL(modgemm_kernel<false>, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+      for (int t = 0; t < c.P && !L.deep; ++t) {
+        if ((tab.p[t] & 1) || tab.p[t] == 256) continue;
+        const int64_t np = (int64_t)L.ksplit * c.batch;
+        const int64_t n = np * (L.outplane_bytes / 16);
+        hipLaunchKernelGGL(tie_fix_kernel, dim3((unsigned)std::min<int64_t>((n + kThreads - 1) / kThreads, 4096)),
+                           dim3(kThreads), 0, s, res8 + t * L.outplane_bytes, L.outplane_bytes, np,
+                           (int64_t)c.P * L.outplane_bytes, tab.p[t]);
+      }
     }
     if (c.ev) {
       if (int st = check_hip(hipEventRecord(c.ev[2], s), "hipEventRecord")) return st;

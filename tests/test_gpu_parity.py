@@ -43,6 +43,29 @@ def test_stage_parity(dev, kind, batch, M, N, K, P, corr):
     check_call(kind, A, B, O.PRIMES[:P], use_corr=corr)
 
 
+MODULI_ORDERS = [
+    # odd first modulus, 256 later: an even digit past the first
+    [255, 256, 253, 251, 247, 241, 239, 233, 229, 227, 223, 217, 211, 199],
+    # even first modulus other than 256: the first digit's own balancing
+    [254, 255, 253, 251, 247, 241, 239, 233, 229, 227, 223, 217, 211, 199],
+    # small moduli (largest quotients in the digit steps), 16 in the middle
+    [7, 11, 13, 16, 9, 5, 17, 19, 23, 29, 31, 37, 41, 43],
+]
+
+
+@pytest.mark.parametrize("order", range(len(MODULI_ORDERS)))
+@pytest.mark.parametrize("kind,M,N,K", [("mm_nt", 70, 90, 700), ("mm_nt", 33, 40, 40_000)])
+def test_moduli_orders(dev, order, kind, M, N, K):
+    """Admissible modulus sets outside the default order run the generic
+    reconstruction, whose digits keep barrett_bal32's balanced range for even
+    moduli; the second shape goes through the K-split fold."""
+    primes = MODULI_ORDERS[order]
+    print(f"case moduli order {order} {kind} {M}x{N}x{K}", flush=True)
+    A = _randn((M, K), 50 + order, dev)
+    B = _randn((K, N), 60 + order, dev)
+    check_call(kind, A, B, primes)
+
+
 def test_inexact_parity(dev):
     print("case inexact mm_nt 96x80x1000", flush=True)
     A = _randn((96, 1000), 5, dev)
