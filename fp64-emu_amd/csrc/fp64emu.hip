@@ -80,7 +80,7 @@ struct ModTables {
   float log2M;                     // float sum of (float)log2(p), as the reference
 };
 
-int inv_mod(int a, int m) {
+__host__ __device__ constexpr int inv_mod(int a, int m) {
   // Extended Euclid on (a mod m, m); m <= 256, gcd 1 by coprimality.
   int r0 = ((a % m) + m) % m, r1 = m, s0 = 1, s1 = 0;
   while (r1 != 0) {
@@ -90,6 +90,40 @@ int inv_mod(int a, int m) {
   }
   return ((s0 % m) + m) % m;
 }
+
+// The reconstruction's per-modulus constants.  Entry t depends only on
+// p_0 .. p_t, so the table of a modulus list serves every prefix of it.
+struct GarnerTab {
+  int p[kMaxP];
+  int minv[kMaxP];                 // (M_t mod p_t)^-1 mod p_t, M_t = prod_{u<t} p_u
+  int nmp[kMaxP * kGarnerWords];   // balanced int8 (-M_u mod p_t) for u < t, 4 per word
+  double invp[kMaxP];              // RN(1 / p)
+};
+
+__host__ __device__ constexpr GarnerTab garner_tables(const int* primes, int P) {
+  GarnerTab T{};
+  for (int t = 0; t < P; ++t) {
+    const int pt = primes[t];
+    T.p[t] = pt;
+    T.invp[t] = 1.0 / (double)pt;
+    long long Mu = 1 % pt;         // M_u mod p_t, running over u
+    for (int u = 0; u < t; ++u) {
+      int bal = (int)((pt - Mu) % pt);   // -M_u mod p_t, balanced
+      if (bal > (pt - 1) / 2) bal -= pt;
+      T.nmp[t * kGarnerWords + (u >> 2)] |= (int)((uint32_t)(uint8_t)(int8_t)bal << (8 * (u & 3)));
+      Mu = (Mu * (primes[u] % pt)) % pt;
+    }
+    T.minv[t] = inv_mod((int)Mu, pt);
+  }
+  return T;
+}
+
+// The reference's modulus list (fp64_emu/__init__.py:20-22), every plan a
+// prefix of it: the modulus-count-specialised reconstruction takes its
+// constants from this table at compile time.
+constexpr int kDefaultModuli[kMaxP] = {256, 255, 253, 251, 247, 241, 239, 233, 229, 227,
+                                       223, 217, 211, 199, 197, 193, 191, 181, 179, 173};
+__device__ constexpr GarnerTab kDefaultTab = garner_tables(kDefaultModuli, kMaxP);
 
 int gcd_int(int a, int b) {
   while (b) { const int t = a % b; a = b; b = t; }
@@ -105,21 +139,17 @@ ModTables make_tables(const int32_t* primes, int P) {
     for (int t = 7 * g; t < std::min(7 * g + 7, P); ++t) prod *= primes[t];
     T.m64[g] = prod;
   }
+  int pr[kMaxP] = {};
+  for (int t = 0; t < P; ++t) pr[t] = primes[t];
+  const GarnerTab G = garner_tables(pr, P);
   float l2 = 0.0f;
   for (int t = 0; t < P; ++t) {
-    const int pt = primes[t];
-    T.p[t] = pt;
-    T.invp[t] = 1.0 / (double)pt;
-    T.c27[t] = (double)((1LL << 27) % pt);
-    l2 += (float)std::log2((double)pt);
-    long long Mu = 1 % pt;   // M_u mod p_t, running over u
-    for (int u = 0; u < t; ++u) {
-      int bal = (int)((pt - Mu) % pt);   // -M_u mod p_t, balanced
-      if (bal > (pt - 1) / 2) bal -= pt;
-      T.nmp[t * kGarnerWords + (u >> 2)] |= (int)((uint32_t)(uint8_t)(int8_t)bal << (8 * (u & 3)));
-      Mu = (Mu * (primes[u] % pt)) % pt;
-    }
-    T.minv[t] = inv_mod((int)Mu, pt);
+    T.p[t] = G.p[t];
+    T.minv[t] = G.minv[t];
+    T.invp[t] = G.invp[t];
+    T.c27[t] = (double)((1LL << 27) % primes[t]);
+    for (int g = 0; g < kGarnerWords; ++g) T.nmp[t * kGarnerWords + g] = G.nmp[t * kGarnerWords + g];
+    l2 += (float)std::log2((double)primes[t]);
   }
   T.log2M = l2;
   return T;
@@ -936,14 +966,20 @@ modgemm_kernel(GemmArgs g) {
             d[q] = v4i{acc_read(acc[x][y][4 * q]), acc_read(acc[x][y][4 * q + 1]),
                        acc_read(acc[x][y][4 * q + 2]), acc_read(acc[x][y][4 * q + 3])};
         } else {
+          // Stage by stage over the block's 16 values: with one wave per
+          // SIMD nothing else hides the latency of a dependent chain.
+          int av[16], qv[16];
+#pragma unroll
+          for (int v = 0; v < 16; ++v) av[v] = acc_read(acc[x][y][v]);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) qv[v] = __double2loint(fma((double)av[v], ip, kMagic));
+          __builtin_amdgcn_sched_barrier(0);
           uint32_t w[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            int r[4];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) r[v] = acc_residue(acc_read(acc[x][y][4 * q + v]), ip, negp);
-            w[q] = pack_bytes(r[0], r[1], r[2], r[3]);
-          }
+          for (int q = 0; q < 4; ++q)
+            w[q] = pack_bytes(__mul24(qv[4 * q], negp) + av[4 * q], __mul24(qv[4 * q + 1], negp) + av[4 * q + 1],
+                              __mul24(qv[4 * q + 2], negp) + av[4 * q + 2], __mul24(qv[4 * q + 3], negp) + av[4 * q + 3]);
           *reinterpret_cast<v4i*>(rdst + blk) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -969,24 +1005,28 @@ modgemm_kernel(GemmArgs g) {
 
 typedef __int128 i128;
 
-// Round-to-nearest-even conversion of a signed 128-bit integer: the top 64
-// significant bits with the dropped tail as a sticky bit (11 positions below
-// the rounding point) convert once.
-__device__ __forceinline__ double i128_to_f64(i128 v) {
-  const bool neg = v < 0;
-  const unsigned __int128 u = neg ? (unsigned __int128)(-v) : (unsigned __int128)v;
-  const uint64_t hi = (uint64_t)(u >> 64), lo = (uint64_t)u;
-  double m;
-  if (hi == 0ull) {
-    m = (double)lo;
-  } else {
-    const int s = 64 - __clzll((long long)hi);      // 1..64 bits above the low word
-    uint64_t top, tail;
-    if (s == 64) { top = hi; tail = lo; }
-    else { top = (hi << (64 - s)) | (lo >> s); tail = lo << (64 - s); }
-    m = ldexp((double)(top | (tail != 0ull ? 1ull : 0ull)), s);
-  }
-  return neg ? -m : m;
+// Exactly rounded (to nearest, ties to even) double of a signed 64-bit integer:
+// the high word scaled by 2^32 is exact, the one fma rounds the sum once.
+__device__ __forceinline__ double i64_to_f64(int64_t v) {
+  return fma((double)(int)(v >> 32), 4294967296.0, (double)(uint32_t)v);
+}
+
+// Round-to-nearest-even double of the two's-complement 128-bit integer
+// w3:w2:w1:w0, scaled by 2^sh.  A value beyond 64 bits is shifted so that its
+// top 64 bits keep 63 significant bits (one sign bit), the dropped tail ORed
+// into the lowest bit (round to odd: floor or ceil, whichever is odd, which
+// rounds to nearest exactly as the full value does, 10 bits below the double's
+// precision); the shift and sh fold into one ldexp of the rounded double.
+__device__ __forceinline__ double i128w_to_f64(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, int sh) {
+  const int64_t hi = (int64_t)(((uint64_t)w3 << 32) | w2);
+  const uint64_t lo = ((uint64_t)w1 << 32) | w0;
+  const uint64_t hs = (uint64_t)(hi ^ (hi >> 63));      // leading zeros = redundant sign bits
+  if (hs == 0 && (int64_t)(hi ^ (int64_t)lo) >= 0)      // the value fits in 64 bits
+    return ldexp(i64_to_f64((int64_t)lo), sh);
+  const int k = hs == 0 ? 63 : __clzll((long long)hs) - 1;   // 0..63
+  uint64_t top = k == 0 ? (uint64_t)hi : ((uint64_t)hi << k) | (lo >> (64 - k));
+  top |= (lo << k) != 0ull ? 1ull : 0ull;
+  return ldexp(i64_to_f64((int64_t)top), 64 - k + sh);
 }
 
 struct ReconArgs {
@@ -1009,8 +1049,8 @@ struct ReconArgs {
 
 // kP: the modulus count fixed at compile time (0: read from the tables), so
 // the digit loops unroll to exactly P steps without guards.  kP > 0 also
-// takes the usual moduli order (first odd or 256, the others odd); kP = 0
-// handles any admissible set.
+// takes the moduli to be the default list's first kP (all odd after 256);
+// kP = 0 handles any admissible list.
 template <bool kExact, bool kDeep, int kP>
 __global__ void __launch_bounds__(kThreads)
 reconstruct_kernel(ReconArgs a) {
@@ -1107,10 +1147,17 @@ reconstruct_kernel(ReconArgs a) {
     }
   }
 
+  // Table entries: compile-time constants of the default modulus list in
+  // the specialised kernels (no scalar registers held across the kernel),
+  // kernel arguments otherwise.
+  auto tab_p = [&](int t) { return kUsual ? kDefaultTab.p[t] : a.tab.p[t]; };
+  auto tab_minv = [&](int t) { return kUsual ? kDefaultTab.minv[t] : a.tab.minv[t]; };
+  auto tab_invp = [&](int t) { return kUsual ? kDefaultTab.invp[t] : a.tab.invp[t]; };
+  auto tab_nmp = [&](int i) { return kUsual ? kDefaultTab.nmp[i] : a.tab.nmp[i]; };
+
   // Garner digits, 4 elements in lockstep.
   int dg[4][kMaxP];
   int dp[4][kGarnerWords];
-  int pv[kMaxP];
 #pragma unroll
   for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -1118,15 +1165,14 @@ reconstruct_kernel(ReconArgs a) {
 #pragma unroll
   for (int t = 0; t < kMaxP; ++t) {
     if (t >= P) continue;
-    const int pt = a.tab.p[t];
-    pv[t] = pt;
+    const int pt = tab_p(t);
     if (t == 0) {
       // M_0 = 1: the first digit is the residue.  The GEMM epilogue and the
       // folds above leave it in [-p/2, (p-1)/2] for odd p (nearest quotient)
       // and for p = 256 (any representative's low byte is that range); any
       // other even p is brought there by the floor rule of barrett_bal32.
       const bool norm = !kUsual && !(pt & 1) && pt != 256;
-      const double pd0 = (double)pt, ip0 = a.tab.invp[0];
+      const double pd0 = (double)pt, ip0 = tab_invp(0);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         int d = (int)(int8_t)(uint8_t)(w[0] >> (8 * e));
@@ -1139,11 +1185,11 @@ reconstruct_kernel(ReconArgs a) {
       }
       continue;
     }
-    const int mi = a.tab.minv[t];
-    const double nip = -a.tab.invp[t];
+    const int mi = tab_minv(t);
+    const double nip = -tab_invp(t);
     int nmw[kGarnerWords];
 #pragma unroll
-    for (int g = 0; g < kGarnerWords; ++g) nmw[g] = (4 * g < t) ? a.tab.nmp[t * kGarnerWords + g] : 0;
+    for (int g = 0; g < kGarnerWords; ++g) nmw[g] = (4 * g < t) ? tab_nmp(t * kGarnerWords + g) : 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       // x = r_t - sum_{u<t} d_u (M_u mod p_t), seeded with r_t (|x| < 2^19).
@@ -1169,6 +1215,11 @@ reconstruct_kernel(ReconArgs a) {
     }
   }
 
+  const int cshift = a.bits_eff[0] - 15;
+  const int sj = (int)a.sftB[b * a.N + j];
+  const int16_t* sA = a.sftA + b * a.M + i0;
+  double* outp = a.out + (b * a.M + i0) * a.N + j;
+
   // Horner per group of 7 (digits 7g .. 7g+6, high to low): group position
   // 6..3 in int32 (four balanced digits stay below 2^31; three below 2^23,
   // so the 24-bit multiply is exact), positions 2..0 in int64.
@@ -1184,14 +1235,12 @@ reconstruct_kernel(ReconArgs a) {
     const int g = t / 7, pos = t % 7;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      if (pos >= 3) h32[e][g] = __mul24(h32[e][g], pv[t]) + dg[e][t];
-      else if (pos == 2) ag[e][g] = (long long)h32[e][g] * pv[t] + dg[e][t];
-      else ag[e][g] = ag[e][g] * pv[t] + dg[e][t];
+      if (pos >= 3) h32[e][g] = __mul24(h32[e][g], tab_p(t)) + dg[e][t];
+      else if (pos == 2) ag[e][g] = (long long)h32[e][g] * tab_p(t) + dg[e][t];
+      else ag[e][g] = ag[e][g] * tab_p(t) + dg[e][t];
     }
   }
 
-  const int cshift = a.bits_eff[0] - 15;
-  const int sj = (int)a.sftB[b * a.N + j];
   const int ng = (P + 6) / 7;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -1200,14 +1249,21 @@ reconstruct_kernel(ReconArgs a) {
     // Every group ends on its position-0 digit, an int64 step, so ag holds
     // the group value whatever the group's digit count.
     const long long a0 = ag[e][0], a1 = ag[e][1], a2 = ag[e][2];
-    const int sh = -((int)a.sftA[b * a.M + i] + sj);
+    const int sh = -((int)sA[e] + sj);
     double val;
     if (kExact) {
       i128 acc = ng == 3 ? (i128)a2 : (ng == 2 ? (i128)a1 : (i128)a0);
       if (ng == 3) acc = acc * (i128)(uint64_t)a.tab.m64[1] + a1;
       if (ng >= 2) acc = acc * (i128)(uint64_t)a.tab.m64[0] + a0;
-      acc += (i128)cv[e] * ((i128)1 << cshift);
-      val = i128_to_f64(acc);
+      // + corr 2^cshift: 1 <= cshift <= 38 (bits_eff in [16, 53]), so the
+      // shifted value is the word pair (cv >> (64 - cshift), cv << cshift).
+      const unsigned __int128 cw =
+          ((unsigned __int128)(uint64_t)(cv[e] >> (64 - cshift)) << 64) | ((uint64_t)cv[e] << cshift);
+      acc = (i128)((unsigned __int128)acc + cw);
+      const unsigned __int128 u = (unsigned __int128)acc;
+      outp[e * a.N] = i128w_to_f64((uint32_t)u, (uint32_t)(u >> 32), (uint32_t)(u >> 64),
+                                   (uint32_t)(u >> 96), sh);
+      continue;
     } else {
       double acc = (double)(ng == 3 ? a2 : (ng == 2 ? a1 : a0));
       if (ng == 3) acc = fma(acc, (double)a.tab.m64[1], (double)a1);
@@ -1215,7 +1271,7 @@ reconstruct_kernel(ReconArgs a) {
       acc = acc + ldexp((double)cv[e], cshift);
       val = acc;
     }
-    a.out[(b * a.M + i) * a.N + j] = ldexp(val, sh);
+    outp[e * a.N] = ldexp(val, sh);
   }
 }
 
@@ -1331,10 +1387,10 @@ int validate_primes(const int32_t* primes, int P) {
 // reconstruction compiled for their exact count; others use the generic one.
 template <bool kExact>
 void launch_reconstruct_p(int P, unsigned grid, hipStream_t s, const ReconArgs& ra) {
-  // The specialised kernels take the first modulus odd or 256 and the others
-  // odd (every prefix of the default set); other sets run the generic one.
-  bool usual = ra.tab.p[0] == 256 || (ra.tab.p[0] & 1);
-  for (int t = 1; t < P; ++t) usual = usual && (ra.tab.p[t] & 1);
+  // The specialised kernels carry the default modulus list's constants;
+  // other lists run the generic one.
+  bool usual = true;
+  for (int t = 0; t < P; ++t) usual = usual && ra.tab.p[t] == kDefaultModuli[t];
   switch (usual ? P : 0) {
 #define FP64EMU_RECON_CASE(n)                                                                 \
     case n:                                                                                   \
