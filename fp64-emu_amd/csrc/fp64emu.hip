@@ -226,6 +226,10 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   L->outplane_bytes = L->chunk_rows * L->Np;
   L->ksplit = L->deep ? 1 : choose_ksplit(batch, ctiles * (L->Np / kTileR), L->Kp / kTileK, P,
                                           L->ncorr);
+  // Under a K-split the two correction products run as two K-deep slots
+  // (two int32 planes): a fused 2K-deep slot would make its groups twice as
+  // long as every residue group (choose_ksplit already counts it as two).
+  if (L->ksplit > 1 && L->ncorr == 1) L->ncorr = 2;
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o = align_up(o + bytes); return at; };
   L->off_sftA = take(sizeof(int16_t) * batch * M);
@@ -348,17 +352,19 @@ size_cols_final_kernel(const double* __restrict__ pmax, const double* __restrict
   const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (j >= totalcols) return;
   double mx = 0.0, ss = 0.0;
-  // Eight slabs' loads in flight; the sum keeps the slab order.
+  // 32 slabs' loads in flight (few columns come with many slabs, up to 128:
+  // the fold is load-latency bound); the sum keeps the slab order.
+  constexpr int kInFlight = 32;
   int s = 0;
-  for (; s + 8 <= nslab; s += 8) {
-    double vm[8], vs[8];
+  for (; s + kInFlight <= nslab; s += kInFlight) {
+    double vm[kInFlight], vs[kInFlight];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < kInFlight; ++u) {
       vm[u] = pmax[(int64_t)(s + u) * totalcols + j];
       vs[u] = pss[(int64_t)(s + u) * totalcols + j];
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < kInFlight; ++u) {
       mx = fmax(mx, vm[u]);
       ss = ss + vs[u];
     }
@@ -1047,11 +1053,13 @@ struct ReconArgs {
   ModTables tab;
 };
 
-// kP: the modulus count fixed at compile time (0: read from the tables), so
-// the digit loops unroll to exactly P steps without guards.  kP > 0 also
+// kSplit: the GEMM ran with a K-split (its own instantiation, so the split
+// sums' registers do not weigh on the common path).  kP: the modulus count
+// fixed at compile time (0: read from the tables), so the digit loops unroll
+// to exactly P steps without guards.  kP > 0 also
 // takes the moduli to be the default list's first kP (all odd after 256);
 // kP = 0 handles any admissible list.
-template <bool kExact, bool kDeep, int kP>
+template <bool kExact, bool kDeep, int kP, bool kSplit>
 __global__ void __launch_bounds__(kThreads)
 reconstruct_kernel(ReconArgs a) {
   const int64_t blk = blockIdx.x;
@@ -1087,32 +1095,52 @@ reconstruct_kernel(ReconArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) cv[e] = c[e];
     }
-  } else if (a.ksplit == 1) {
+  } else if (!kSplit) {
 #pragma unroll
     for (int t = 0; t < kMaxP; ++t)
       if (t < P) w[t] = *reinterpret_cast<const uint32_t*>(a.res8 + (b * P + t) * a.outplane + boff);
   } else {
     // K-split: the S partial residues sum (|sum| <= 128 S) and fold to the
-    // residue (any representative serves: each digit reduces mod p again).
-    // Split-outer, plane-inner: the P loads of one split are independent.
+    // residue (any representative serves: each digit reduces mod p again),
+    // and the S x ncorr correction parts add up.  Two splits per iteration
+    // (S is a power of two >= 2), residues and corrections together, so the
+    // loads share each round trip.
     int sums[kMaxP][4];
 #pragma unroll
     for (int t = 0; t < kMaxP; ++t)
 #pragma unroll
       for (int e = 0; e < 4; ++e) sums[t][e] = 0;
-    for (int sp = 0; sp < a.ksplit; ++sp) {
-      uint32_t u[kMaxP];
+    for (int sp = 0; sp < a.ksplit; sp += 2) {
+      uint32_t u[2][kMaxP];
+      v4i cw[2][2];
 #pragma unroll
-      for (int t = 0; t < kMaxP; ++t)
-        if (t < P)
-          u[t] = *reinterpret_cast<const uint32_t*>(
-              a.res8 + ((sp * a.batch + b) * P + t) * a.outplane + boff);
+      for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int t = 0; t < kMaxP; ++t)
-        if (t < P) {
+        for (int t = 0; t < kMaxP; ++t)
+          if (t < P)
+            u[h][t] = *reinterpret_cast<const uint32_t*>(
+                a.res8 + (((sp + h) * a.batch + b) * P + t) * a.outplane + boff);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) sums[t][e] += (int)(int8_t)(uint8_t)(u[t] >> (8 * e));
-        }
+        for (int cc = 0; cc < 2; ++cc)
+          if (cc < a.ncorr)
+            cw[h][cc] = *reinterpret_cast<const v4i*>(
+                a.corr + (((sp + h) * a.batch + b) * a.ncorr + cc) * a.outplane + boff);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int t = 0; t < kMaxP; ++t)
+          if (t < P) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sums[t][e] += (int)(int8_t)(uint8_t)(u[h][t] >> (8 * e));
+          }
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+          if (cc < a.ncorr) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cv[e] += cw[h][cc][e];
+          }
+      }
     }
 #pragma unroll
     for (int t = 0; t < kMaxP; ++t)
@@ -1128,15 +1156,7 @@ reconstruct_kernel(ReconArgs a) {
         w[t] = u;
       }
   }
-  if (!kDeep && a.ncorr > 0 && a.ksplit > 1) {
-    for (int sp = 0; sp < a.ksplit; ++sp)
-      for (int cc = 0; cc < a.ncorr; ++cc) {
-        const v4i c1 = *reinterpret_cast<const v4i*>(
-            a.corr + ((sp * a.batch + b) * a.ncorr + cc) * a.outplane + boff);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) cv[e] += c1[e];
-      }
-  } else if (!kDeep && a.ncorr > 0) {
+  if (!kDeep && !kSplit && a.ncorr > 0) {   // (a K-split summed them above)
     const v4i c1 = *reinterpret_cast<const v4i*>(a.corr + (b * a.ncorr) * a.outplane + boff);
 #pragma unroll
     for (int e = 0; e < 4; ++e) cv[e] = c1[e];
@@ -1385,31 +1405,37 @@ int validate_primes(const int32_t* primes, int P) {
 
 // Modulus counts of the planner (plan_config: 14-15; plan: up to 20) get a
 // reconstruction compiled for their exact count; others use the generic one.
-template <bool kExact>
+template <bool kExact, bool kSplit>
 void launch_reconstruct_p(int P, unsigned grid, hipStream_t s, const ReconArgs& ra) {
   // The specialised kernels carry the default modulus list's constants;
   // other lists run the generic one.
   bool usual = true;
   for (int t = 0; t < P; ++t) usual = usual && ra.tab.p[t] == kDefaultModuli[t];
   switch (usual ? P : 0) {
-#define FP64EMU_RECON_CASE(n)                                                                 \
-    case n:                                                                                   \
-      hipLaunchKernelGGL((reconstruct_kernel<kExact, false, n>), dim3(grid), dim3(kThreads),  \
-                         0, s, ra);                                                           \
+#define FP64EMU_RECON_CASE(n)                                                                   \
+    case n:                                                                                     \
+      hipLaunchKernelGGL((reconstruct_kernel<kExact, false, n, kSplit>), dim3(grid),            \
+                         dim3(kThreads), 0, s, ra);                                             \
       return;
     FP64EMU_RECON_CASE(12) FP64EMU_RECON_CASE(13) FP64EMU_RECON_CASE(14)
     FP64EMU_RECON_CASE(15) FP64EMU_RECON_CASE(16) FP64EMU_RECON_CASE(17)
     FP64EMU_RECON_CASE(18) FP64EMU_RECON_CASE(19) FP64EMU_RECON_CASE(20)
 #undef FP64EMU_RECON_CASE
     default:
-      hipLaunchKernelGGL((reconstruct_kernel<kExact, false, 0>), dim3(grid), dim3(kThreads), 0,
-                         s, ra);
+      hipLaunchKernelGGL((reconstruct_kernel<kExact, false, 0, kSplit>), dim3(grid), dim3(kThreads),
+                         0, s, ra);
   }
 }
 
 void launch_reconstruct(bool exact, int P, unsigned grid, hipStream_t s, const ReconArgs& ra) {
-  if (exact) launch_reconstruct_p<true>(P, grid, s, ra);
-  else launch_reconstruct_p<false>(P, grid, s, ra);
+  const bool split = ra.ksplit > 1;
+  if (exact) {
+    if (split) launch_reconstruct_p<true, true>(P, grid, s, ra);
+    else launch_reconstruct_p<true, false>(P, grid, s, ra);
+  } else {
+    if (split) launch_reconstruct_p<false, true>(P, grid, s, ra);
+    else launch_reconstruct_p<false, false>(P, grid, s, ra);
+  }
 }
 
 int run(const Call& c) {
@@ -1590,9 +1616,9 @@ int run(const Call& c) {
     const unsigned grid = (unsigned)ra.nblocks;
     if (L.deep) {
       if (c.exact)
-        hipLaunchKernelGGL((reconstruct_kernel<true, true, 0>), dim3(grid), dim3(kThreads), 0, s, ra);
+        hipLaunchKernelGGL((reconstruct_kernel<true, true, 0, false>), dim3(grid), dim3(kThreads), 0, s, ra);
       else
-        hipLaunchKernelGGL((reconstruct_kernel<false, true, 0>), dim3(grid), dim3(kThreads), 0, s, ra);
+        hipLaunchKernelGGL((reconstruct_kernel<false, true, 0, false>), dim3(grid), dim3(kThreads), 0, s, ra);
     } else {
       launch_reconstruct(c.exact, c.P, grid, s, ra);
     }

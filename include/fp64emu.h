@@ -128,7 +128,8 @@ int fp64emu_mm_nt_events(double* out, const double* A, const double* Bt, int64_t
 typedef struct {
   int64_t batch, M, N, K;   /* per batch member */
   int nprimes, use_corr;
-  int ncorr;                /* int32 correction planes per member: 1 (fused, K <= 65536) or 2 */
+  int ncorr;                /* int32 correction planes per member: 1 (fused, K <= 65536 and
+                               ksplit 1) or 2 */
   int nslab;                /* column-sizing slabs for a [K,N] operand */
   int deep;                 /* K > 131071: the K-segmented form (mm / bmm only) */
   int nseg;                 /* K segments (1 unless deep) */

@@ -80,7 +80,7 @@ def test_layout_consistency(shape, P, corr):
     deep = K > 131071
     assert L.deep == int(deep) and L.nseg == ((K + 65535) // 65536 if deep else 1)
     assert L.kseg == (65536 if deep else K)
-    assert L.ncorr == (0 if not corr else (1 if (deep or K <= 65536) else 2))
+    assert L.ncorr == (0 if not corr else (1 if (deep or (K <= 65536 and L.ksplit == 1)) else 2))
     nplanes = P + (2 if corr else 0)
     assert L.planeA_bytes == L.Mp * L.Kp and L.planeB_bytes == L.Np * L.Kp
     assert L.memberA_bytes == nplanes * L.planeA_bytes

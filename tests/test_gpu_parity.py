@@ -161,3 +161,22 @@ def test_row_chunks_match_full(dev, kind, M, N, K):
         assert torch.equal(out, full), f"workspace {wbytes}"
     with pytest.raises(capi.CapiError, match="workspace too small"):
         capi.run(kind, A, B, O.PRIMES[:P], ws=torch.empty(wmin - 256, dtype=torch.uint8, device=dev))
+
+
+@pytest.mark.parametrize("order", [1, 2])
+def test_deep_k_moduli_orders(dev, order):
+    """K-segmented path with a modulus list outside the default: the
+    segment residue sums fold in the generic reconstruction (an even first
+    modulus other than 256; small moduli)."""
+    from parity_util import bits_equal
+    from fp64_emu import capi
+    primes = MODULI_ORDERS[order]
+    M, N, K = 8, 12, 140_000
+    print(f"case deep-K moduli order {order} mm {M}x{N}x{K}", flush=True)
+    A = _randn((M, K), 90 + order, dev)
+    B = _randn((N, K), 95 + order, dev)
+    out, ws, lay = capi.run("mm", A, B, primes)
+    torch.cuda.synchronize()
+    assert lay.deep == 1
+    oout, info = O.mm(A.cpu().numpy(), B.cpu().numpy(), 0, primes)
+    assert bits_equal(out.cpu().numpy(), oout), "deep-K output differs from the oracle"
