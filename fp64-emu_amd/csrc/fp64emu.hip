@@ -507,6 +507,26 @@ extract_kernel(ExtractArgs a) {
   const int64_t k0 = kt * kTileK + (wave & 1) * 32 + (lane >> 5) * 16;  // first of 16 k
   const bool rowok = r < R;
 
+  // A fragment that is all padding (its 32 rows or its 32 k past the
+  // operand) only stores zeros: no loads and no residue arithmetic.
+  const int P = a.tab.P;
+  const int64_t nkt = a.nkt;
+  const int64_t rt = rblk >> 3, fr = (rblk & 7) * 2 + (wave & 1);
+  const int64_t plane = isA ? a.planeA : a.planeB;
+  int8_t* base = (isA ? a.planesA : a.planesB) + b * (isA ? a.memberA : a.memberB);
+  const int64_t off = (rt * nkt + kt) * kTileBytes + fr * kFragBytes + lane * 16;
+  if (__builtin_amdgcn_readfirstlane((int)(rblk * 32 >= R || kt * kTileK + (wave & 1) * 32 >= K))) {
+    const v4i z = v4i{0, 0, 0, 0};
+    for (int pi = 0; pi < P; ++pi) *reinterpret_cast<v4i*>(base + pi * plane + off) = z;
+    if (a.use_corr) {
+      int8_t* cb = base + (int64_t)P * plane;
+      const int64_t o1 = (rt * 2 * nkt + kt) * kTileBytes + fr * kFragBytes + lane * 16;
+      *reinterpret_cast<v4i*>(cb + o1) = z;
+      *reinterpret_cast<v4i*>(cb + o1 + nkt * kTileBytes) = z;
+    }
+    return;
+  }
+
   // Shift: per row of A / of B [N,K]; per column of B [K,N] -- one per lane.
   const int16_t* sfts = isA ? a.sftA : a.sftB;
   const int shift = rowok ? (int)sfts[b * R + r] : 0;
@@ -561,12 +581,6 @@ extract_kernel(ExtractArgs a) {
 
   // One plane at a time: 16 residues -> one 16-byte chunk per lane, 1 KiB
   // contiguous per wave.
-  const int P = a.tab.P;
-  const int64_t nkt = a.nkt;
-  const int64_t rt = rblk >> 3, fr = (rblk & 7) * 2 + (wave & 1);
-  const int64_t plane = isA ? a.planeA : a.planeB;
-  int8_t* base = (isA ? a.planesA : a.planesB) + b * (isA ? a.memberA : a.memberB);
-  const int64_t off = (rt * nkt + kt) * kTileBytes + fr * kFragBytes + lane * 16;
   // rr = v - p RNE(v/p) lies in [-p/2, p/2]: balanced for odd p, and for
   // p = 256 the byte of +128 is that of -128.  Another even p turns a tie's
   // +p/2 into barrett_bal32's -p/2 (a separate copy of the loop, so the
