@@ -449,10 +449,11 @@ pick_width_kernel(const float* __restrict__ lgA, int64_t m, const float* __restr
 // the reference's -128.
 //
 // Plane layout (per batch member, per plane): 256-row x 64-k tiles, row tile
-// major, k tile minor; a tile holds 16 fragments of 32 rows x 32 k, fragment
-// f = 2 * (row % 256 / 32) + (k % 64 / 32), each 1 KiB in the operand order of
-// v_mfma_i32_32x32x32_i8: lane l = 32 * (k % 32 / 16) + (row % 32) holds
-// k % 16 at byte 16 * l + k % 16.  The correction plane is one 2*Kp-deep
+// major, k tile minor; a tile holds 16 fragments of 16 rows x 64 k, fragment
+// f = row % 256 / 16, each 1 KiB in the operand order of
+// v_mfma_i32_16x16x64_i8: lane l = 16 * (k % 64 / 16) + (row % 16) holds
+// k % 16 at byte 16 * l + k % 16 (A's rows and B's columns alike, so any
+// order of the 16 k inside a lane pairs up in the dot product).  The correction plane is one 2*Kp-deep
 // plane: A = [hi7 | q7], B = [q7 | hi7], so one GEMM accumulates
 // hi7_A q7_B^T + q7_A hi7_B^T.
 
@@ -500,22 +501,22 @@ extract_kernel(ExtractArgs a) {
   }
   const int64_t R = isA ? a.M : a.N;
   const int64_t K = a.K;
-  // Wave w covers rows 64 rg + 32 (w >> 1) .. +32 and k half (w & 1) of the
-  // k tile: one 32x32 fragment.
-  const int64_t rblk = rg * 2 + (wave >> 1);                     // 32-row block
-  const int64_t r = rblk * 32 + (lane & 31);                     // plane row (A row or B column)
-  const int64_t k0 = kt * kTileK + (wave & 1) * 32 + (lane >> 5) * 16;  // first of 16 k
+  // Wave w covers rows 64 rg + 16 w .. +16 and the whole k tile: one
+  // 16 x 64 fragment, lane l = 16 (k / 16) + row % 16 holding 16 k.
+  const int64_t rblk = rg * 4 + wave;                            // 16-row block
+  const int64_t r = rblk * 16 + (lane & 15);                     // plane row (A row or B column)
+  const int64_t k0 = kt * kTileK + (lane >> 4) * 16;             // first of 16 k
   const bool rowok = r < R;
 
-  // A fragment that is all padding (its 32 rows or its 32 k past the
+  // A fragment that is all padding (its 16 rows or its 64 k past the
   // operand) only stores zeros: no loads and no residue arithmetic.
   const int P = a.tab.P;
   const int64_t nkt = a.nkt;
-  const int64_t rt = rblk >> 3, fr = (rblk & 7) * 2 + (wave & 1);
+  const int64_t rt = rblk >> 4, fr = rblk & 15;
   const int64_t plane = isA ? a.planeA : a.planeB;
   int8_t* base = (isA ? a.planesA : a.planesB) + b * (isA ? a.memberA : a.memberB);
   const int64_t off = (rt * nkt + kt) * kTileBytes + fr * kFragBytes + lane * 16;
-  if (__builtin_amdgcn_readfirstlane((int)(rblk * 32 >= R || kt * kTileK + (wave & 1) * 32 >= K))) {
+  if (__builtin_amdgcn_readfirstlane((int)(rblk * 16 >= R || kt * kTileK >= K))) {
     const v4i z = v4i{0, 0, 0, 0};
     for (int pi = 0; pi < P; ++pi) *reinterpret_cast<v4i*>(base + pi * plane + off) = z;
     if (a.use_corr) {
@@ -630,8 +631,9 @@ extract_kernel(ExtractArgs a) {
 // modulus slots (the reference's bal8, :613-620, here as an exact fp64
 // nearest-quotient reduction), raw int32 for correction slots.
 //
-// 4 waves in a 2x2 arrangement, 128x128 per wave = 4x4 v_mfma_i32_32x32x32_i8
-// tiles (256 accumulator registers).  Operand tiles stream into a 4-stage LDS
+// 4 waves in a 2x2 arrangement, 128x128 per wave = 8x8 v_mfma_i32_16x16x64_i8
+// tiles (256 accumulator registers; the 16x16 form draws less power per
+// operation than 32x32x32, so under the power cap the clock runs higher).  Operand tiles stream into a 4-stage LDS
 // ring with direct global->LDS copies (prefetch distance 3 k-steps); the
 // planes are stored in fragment order, so each stage is a linear copy and
 // every fragment read is 16 contiguous bytes per lane (bank-conflict free).
@@ -639,10 +641,10 @@ extract_kernel(ExtractArgs a) {
 // run, the fragments of kt+1 are read, so LDS latency stays off the MFMA
 // path.  One explicit wait + barrier per k-step.
 //
-// Output blocks (res8 / corr planes): 32x32 blocks, row-block major; inside
-// a block, lane l holds 16 elements in the MFMA accumulator order --
-// element v of lane l is (row 8*(v/4) + 4*(l/32) + v%4, column l%32) -- as
-// 16 consecutive bytes (int8) or 16 consecutive int32.
+// Output blocks (res8 / corr planes): 16 rows x 64 columns, row-block major;
+// element 16 l + 4 q + v of a block (lane l, accumulator column block q,
+// value v) is row 4 (l / 16) + v, column 16 q + l % 16: 16 consecutive bytes
+// (int8) or int32 per lane.
 
 struct GemmArgs {
   const int8_t* A;
@@ -663,7 +665,6 @@ struct GemmArgs {
   double invp[kMaxP];
 };
 
-typedef int v16i __attribute__((ext_vector_type(16)));
 
 // s_waitcnt immediate (gfx9 encoding): wait until at most `vm` vector-memory
 // operations of this wave are outstanding and all LDS operations are done.
@@ -711,6 +712,30 @@ __device__ __forceinline__ uint32_t pack_bytes(int r0, int r1, int r2, int r3) {
   const uint32_t lo = __builtin_amdgcn_perm((uint32_t)r1, (uint32_t)r0, 0x0c0c0400u);
   const uint32_t hi = __builtin_amdgcn_perm((uint32_t)r3, (uint32_t)r2, 0x0c0c0400u);
   return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+// One v_mfma_i32_16x16x64_i8 accumulating in place.  Inline assembly ties
+// the accumulator to the destination: through the builtin the compiler
+// renamed the 64 accumulator quads between k-steps and copied them back
+// (hundreds of v_accvgpr_mov per step).  The hardware chains MFMAs on one
+// accumulator; the wait states a compiler would place around MFMAs it can
+// see are placed by hand with mfma_fence where the accumulators are written
+// or read by other instructions.
+__device__ __forceinline__ void mma16(v4i& acc, const v4i& a, const v4i& b) {
+  asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// The first k-step's form: the accumulator input is the constant 0, so no
+// other instruction ever writes an accumulator an MFMA then reads.
+__device__ __forceinline__ void mma16_init(v4i& acc, const v4i& a, const v4i& b) {
+  asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, 0" : "=a"(acc) : "v"(a), "v"(b));
+}
+
+// 32 wait states, fenced against scheduling: more than any MFMA needs between
+// its result and another instruction's read of it.
+__device__ __forceinline__ void mfma_fence() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 constexpr int kStages = 4;                   // LDS ring: 4 x 32 KiB
@@ -782,8 +807,8 @@ modgemm_kernel(GemmArgs g) {
     __builtin_amdgcn_global_load_lds(b_, st_ + kTileBytes, 16, 2048, 0);               \
     __builtin_amdgcn_global_load_lds(b_, st_ + kTileBytes, 16, 3072, 0);               \
   } while (0)
-  // Fragments of one k-step: F[0..7] = A row blocks 4 wm .. 4 wm + 3 (both k
-  // halves), F[8..15] = the same for B.
+  // Fragments of one k-step: F[0..7] = A row blocks 8 wm .. 8 wm + 7 (16 rows
+  // x 64 k each), F[8..15] = the same for B.
 #define FP64EMU_READF(F, kt)                                                               \
   do {                                                                                     \
     const v4i* sa_ = reinterpret_cast<const v4i*>(lds + ((kt) & (kStages - 1)) * kStageBytes); \
@@ -791,36 +816,30 @@ modgemm_kernel(GemmArgs g) {
     _Pragma("unroll") for (int y = 0; y < 8; ++y) F[8 + y] = sb_[(wn * 8 + y) * 64 + lane]; \
     _Pragma("unroll") for (int x = 0; x < 8; ++x) F[x] = sa_[(wm * 8 + x) * 64 + lane];     \
   } while (0)
-#define FP64EMU_MMA(F)                                                                      \
+#define FP64EMU_MMA(F, MMA)                                                                 \
   do {                                                                                      \
-    _Pragma("unroll") for (int h = 0; h < 2; ++h)                                           \
-    _Pragma("unroll") for (int x = 0; x < 4; ++x)                                           \
-    _Pragma("unroll") for (int y = 0; y < 4; ++y)                                           \
-      acc[x][y] = __builtin_amdgcn_mfma_i32_32x32x32_i8(F[2 * x + h], F[8 + 2 * y + h],     \
-                                                         acc[x][y], 0, 0, 0);               \
+    _Pragma("unroll") for (int x = 0; x < 8; ++x)                                           \
+    _Pragma("unroll") for (int y = 0; y < 8; ++y) MMA(acc[x][y], F[x], F[8 + y]);           \
   } while (0)
   // One k-step: stage kt+1 must have landed (own copies: at most one later
   // group in flight), then the barrier makes every wave's copies visible
   // and guarantees every wave finished reading the stage refilled next.
-#define FP64EMU_STEP(kt, FC, FN)                                                         \
+#define FP64EMU_STEP(kt, FC, FN, MMA)                                                    \
   do {                                                                                   \
     if ((kt) + 3 <= nk) wait_vm_lgkm0<kDmaPerStep>(); else wait_vm_lgkm0<0>();           \
     barrier_lds();                                                                       \
     if ((kt) + 3 < nk) FP64EMU_ISSUE((kt) + 3);                                          \
     FP64EMU_READF(FN, (kt) + 1);                                                         \
-    FP64EMU_MMA(FC);                                                                     \
-    _Pragma("unroll") for (int q = 0; q < 16; ++q) {                                     \
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                 \
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                                 \
-    }                                                                                    \
+    FP64EMU_MMA(FC, MMA);                                                                \
   } while (0)
   // Steady-state step (a copy for step kt+3 exists): an unconditional wait,
   // so the compiler's own wait tracking sees every earlier fragment read
   // retired (a conditional wait made it stall on the first read of each
-  // step), and the step in four fenced chunks, each {2 copies, 4 fragment
-  // reads, 8 MFMAs}: the copies reach the texture unit spread over the step
-  // instead of as a burst of 32 after the barrier, which delayed the last
-  // wave's MFMAs and made every wave wait for it at the next barrier.
+  // step), and the step in four fenced chunks, each {2 copies, then 4 times
+  // one fragment read and 4 MFMAs}: the copies reach the texture unit spread
+  // over the step instead of as a burst after the barrier, which delayed the
+  // last wave's MFMAs and made every wave wait for it at the next barrier,
+  // and each read has 4 MFMAs to land behind.
 #define FP64EMU_DMA2(kt, c)                                                                  \
   do {                                                                                       \
     lds_i8* st_ = (lds_i8*)(lds + ((kt) & (kStages - 1)) * kStageBytes + wave * 4096 +       \
@@ -829,107 +848,106 @@ modgemm_kernel(GemmArgs g) {
     __builtin_amdgcn_global_load_lds(g_, st_, 16, ((c) & 1) * 2048, 0);                      \
     __builtin_amdgcn_global_load_lds(g_, st_, 16, ((c) & 1) * 2048 + 1024, 0);               \
   } while (0)
-#define FP64EMU_READ4(F, kt, c)                                                              \
+  // Chunk c: MFMAs of A blocks 2c, 2c+1 against all 8 B blocks; reads of the
+  // next step's fragments 4c .. 4c+3 (B 0..7, then A 0..7), so the first
+  // chunk of the next step finds its operands read a step ahead.
+#define FP64EMU_CHUNK(kt, FC, FN, c, MMA)                                                    \
   do {                                                                                       \
-    const v4i* sa_ = reinterpret_cast<const v4i*>(lds + ((kt) & (kStages - 1)) * kStageBytes); \
+    FP64EMU_DMA2((kt) + 3, c);                                                               \
+    __builtin_amdgcn_sched_barrier(0);                                                       \
+    const v4i* sa_ = reinterpret_cast<const v4i*>(lds + (((kt) + 1) & (kStages - 1)) * kStageBytes); \
     const v4i* sb_ = sa_ + kTileBytes / 16;                                                  \
     _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                          \
       const int f_ = (c) * 4 + j;                                                            \
-      if (f_ < 8) F[8 + f_] = sb_[(wn * 8 + f_) * 64 + lane];                                \
-      else F[f_ - 8] = sa_[(wm * 8 + f_ - 8) * 64 + lane];                                   \
+      if (f_ < 8) FN[8 + f_] = sb_[(wn * 8 + f_) * 64 + lane];                               \
+      else FN[f_ - 8] = sa_[(wm * 8 + f_ - 8) * 64 + lane];                                  \
+      __builtin_amdgcn_sched_barrier(0);                                                     \
+      _Pragma("unroll") for (int u = 0; u < 4; ++u) {                                        \
+        const int m_ = 4 * j + u, x = (c) * 2 + m_ / 8, y = m_ % 8;                          \
+        MMA(acc[x][y], FC[x], FC[8 + y]);                                                    \
+      }                                                                                      \
+      __builtin_amdgcn_sched_barrier(0);                                                     \
     }                                                                                        \
   } while (0)
-#define FP64EMU_MMA8(F, c)                                                                   \
-  do {                                                                                       \
-    _Pragma("unroll") for (int xx = 0; xx < 2; ++xx)                                         \
-    _Pragma("unroll") for (int y = 0; y < 4; ++y) {                                          \
-      const int x = ((c) & 1) * 2 + xx, h = (c) >> 1;                                        \
-      acc[x][y] = __builtin_amdgcn_mfma_i32_32x32x32_i8(F[2 * x + h], F[8 + 2 * y + h],      \
-                                                         acc[x][y], 0, 0, 0);                \
-    }                                                                                        \
-  } while (0)
-#define FP64EMU_CHUNK(kt, FC, FN, c)                                                         \
-  do {                                                                                       \
-    FP64EMU_DMA2((kt) + 3, c);                                                               \
-    FP64EMU_READ4(FN, (kt) + 1, c);                                                          \
-    FP64EMU_MMA8(FC, c);                                                                     \
-    __builtin_amdgcn_sched_group_barrier(0x010, 2, 0);                                       \
-    _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                          \
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                     \
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                                     \
-    }                                                                                        \
-    __builtin_amdgcn_sched_barrier(0);                                                       \
-  } while (0)
-#define FP64EMU_STEP_FULL(kt, FC, FN)                                                        \
+#define FP64EMU_STEP_FULL(kt, FC, FN, MMA)                                                   \
   do {                                                                                       \
     wait_vm_lgkm0<kDmaPerStep>();                                                            \
     barrier_lds();                                                                           \
-    FP64EMU_CHUNK(kt, FC, FN, 0);                                                            \
-    FP64EMU_CHUNK(kt, FC, FN, 1);                                                            \
-    FP64EMU_CHUNK(kt, FC, FN, 2);                                                            \
-    FP64EMU_CHUNK(kt, FC, FN, 3);                                                            \
+    FP64EMU_CHUNK(kt, FC, FN, 0, MMA);                                                       \
+    FP64EMU_CHUNK(kt, FC, FN, 1, MMA);                                                       \
+    FP64EMU_CHUNK(kt, FC, FN, 2, MMA);                                                       \
+    FP64EMU_CHUNK(kt, FC, FN, 3, MMA);                                                       \
   } while (0)
 
-  v16i acc[4][4];
+  v4i acc[8][8];
+  if (nk == 0) {
+    // A trailing K-split group past the end: its outputs are zeros.
 #pragma unroll
-  for (int x = 0; x < 4; ++x)
+    for (int x = 0; x < 8; ++x)
 #pragma unroll
-    for (int y = 0; y < 4; ++y) acc[x][y] = v16i{};
-
+      for (int y = 0; y < 8; ++y) acc[x][y] = v4i{0, 0, 0, 0};
+  } else {
 #pragma unroll
-  for (int s = 0; s < kStages - 1; ++s)
-    if (s < nk) FP64EMU_ISSUE(s);
-  v4i F0[16], F1[16];
-  if (nk > 0) {
+    for (int s = 0; s < kStages - 1; ++s)
+      if (s < nk) FP64EMU_ISSUE(s);
+    v4i F0[16], F1[16];
     wait_vm_lgkm0<0>();
     barrier_lds();
     FP64EMU_READF(F0, 0);
-  }
-  // Reading fragments of k-step nk (one past the end) touches a stale stage
-  // and is never used; no copy targets it.
-  int kt = 0;
-  for (; kt + 2 <= nk - 3; kt += 2) {        // copies for kt + 3 and kt + 4 exist
-    FP64EMU_STEP_FULL(kt, F0, F1);
-    FP64EMU_STEP_FULL(kt + 1, F1, F0);
-  }
-  for (; kt + 2 <= nk; kt += 2) {
-    FP64EMU_STEP(kt, F0, F1);
-    FP64EMU_STEP(kt + 1, F1, F0);
-  }
-  if (kt < nk) {
+    // k-step 0 starts the accumulators; then pairs of steps alternate the
+    // fragment buffers.  Reading fragments of k-step nk (one past the end)
+    // touches a stale stage and is never used; no copy targets it.
+    if (nk >= 4) FP64EMU_STEP_FULL(0, F0, F1, mma16_init);
+    else FP64EMU_STEP(0, F0, F1, mma16_init);
+    int kt = 1;
+    for (; kt + 2 <= nk - 3; kt += 2) {      // copies for kt + 3 and kt + 4 exist
+      FP64EMU_STEP_FULL(kt, F1, F0, mma16);
+      FP64EMU_STEP_FULL(kt + 1, F0, F1, mma16);
+    }
+    for (; kt + 2 <= nk; kt += 2) {
+      FP64EMU_STEP(kt, F1, F0, mma16);
+      FP64EMU_STEP(kt + 1, F0, F1, mma16);
+    }
+    if (kt < nk) {
+      wait_vm_lgkm0<0>();
+      FP64EMU_MMA(F1, mma16);
+    }
+    // No copy may still target this work group's LDS when it retires.
     wait_vm_lgkm0<0>();
-    FP64EMU_MMA(F0);
+    mfma_fence();   // the last MFMAs' results before anything reads them
   }
-  // No copy may still target this work group's LDS when it retires.
-  wait_vm_lgkm0<0>();
 #undef FP64EMU_ISSUE
 #undef FP64EMU_READF
 #undef FP64EMU_MMA
 #undef FP64EMU_STEP
 #undef FP64EMU_DMA2
-#undef FP64EMU_READ4
-#undef FP64EMU_MMA8
 #undef FP64EMU_CHUNK
 #undef FP64EMU_STEP_FULL
 
-  // Epilogue: 32x32 blocks (mb, nb) of this wave, 16 values per lane.
-  const int64_t NB = (int64_t)g.TN * 8;                 // 32-blocks per output row
-  const int64_t mb0 = (int64_t)mt * 8 + wm * 4, nb0 = (int64_t)nt * 8 + wn * 4;
+  // Epilogue: output blocks of 16 rows x 64 columns; this wave's 128 x 128
+  // holds 8 row blocks x 2 column blocks.  Element 16 l + 4 q + v of a
+  // block is lane l's value v of accumulator column block q (row
+  // 4 (l / 16) + v, column 16 q + l % 16).
+  const int64_t NB = (int64_t)g.TN * 4;                 // 64-column blocks per output row
+  const int64_t rb0 = (int64_t)mt * 16 + wm * 8, cb0 = (int64_t)nt * 4 + wn * 2;
   if (kDeep && is_corr) {
     // K-segmented: this segment's correction products join the int64 sum.
     typedef long long v2l __attribute__((ext_vector_type(2)));
     int64_t* dst = g.cacc + b * g.outplane;
 #pragma unroll
-    for (int x = 0; x < 4; ++x)
+    for (int x = 0; x < 8; ++x)
 #pragma unroll
-      for (int y = 0; y < 4; ++y) {
-        v2l* d = reinterpret_cast<v2l*>(dst + ((mb0 + x) * NB + nb0 + y) * 1024 + lane * 16);
+      for (int h = 0; h < 2; ++h) {
+        v2l* d = reinterpret_cast<v2l*>(dst + ((rb0 + x) * NB + cb0 + h) * 1024 + lane * 16);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          v2l v = v2l{(long long)acc[x][y][2 * q], (long long)acc[x][y][2 * q + 1]};
-          if (!g.first) v += d[q];
-          d[q] = v;
-        }
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            v2l v = v2l{(long long)acc_read(acc[x][4 * h + q][2 * u]),
+                        (long long)acc_read(acc[x][4 * h + q][2 * u + 1])};
+            if (!g.first) v += d[2 * q + u];
+            d[2 * q + u] = v;
+          }
         __builtin_amdgcn_sched_barrier(0);
       }
   } else if (kDeep) {
@@ -942,16 +960,16 @@ modgemm_kernel(GemmArgs g) {
     const int half_lo = -(g.p[t] >> 1);
     int32_t* dst = g.racc + (b * g.P + t) * g.outplane;
 #pragma unroll
-    for (int x = 0; x < 4; ++x)
+    for (int x = 0; x < 8; ++x)
 #pragma unroll
-      for (int y = 0; y < 4; ++y) {
-        v4i* d = reinterpret_cast<v4i*>(dst + ((mb0 + x) * NB + nb0 + y) * 1024 + lane * 16);
+      for (int h = 0; h < 2; ++h) {
+        v4i* d = reinterpret_cast<v4i*>(dst + ((rb0 + x) * NB + cb0 + h) * 1024 + lane * 16);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           v4i v;
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            int r = acc_residue(acc[x][y][4 * q + u], ip, negp);
+            int r = acc_residue(acc_read(acc[x][4 * h + q][u]), ip, negp);
             if (tie_fix) r = r == half_lo ? -half_lo : r;
             // +p/2 (p = 256) is -p/2 in the balanced range: the int8 value
             v[u] = (int)(int8_t)r;
@@ -975,22 +993,22 @@ modgemm_kernel(GemmArgs g) {
     int32_t* cdst = g.corr + (sbm * g.ncorr + (is_corr ? slot : 0)) * g.outplane;
     int8_t* rdst = g.res8 + (sbm * g.P + t) * g.outplane;
 #pragma unroll
-    for (int x = 0; x < 4; ++x)
+    for (int x = 0; x < 8; ++x)
 #pragma unroll
-      for (int y = 0; y < 4; ++y) {
-        const int64_t blk = ((mb0 + x) * NB + nb0 + y) * 1024 + lane * 16;
+      for (int h = 0; h < 2; ++h) {
+        const int64_t blk = ((rb0 + x) * NB + cb0 + h) * 1024 + lane * 16;
         if (is_corr) {
           v4i* d = reinterpret_cast<v4i*>(cdst + blk);
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            d[q] = v4i{acc_read(acc[x][y][4 * q]), acc_read(acc[x][y][4 * q + 1]),
-                       acc_read(acc[x][y][4 * q + 2]), acc_read(acc[x][y][4 * q + 3])};
+            d[q] = v4i{acc_read(acc[x][4 * h + q][0]), acc_read(acc[x][4 * h + q][1]),
+                       acc_read(acc[x][4 * h + q][2]), acc_read(acc[x][4 * h + q][3])};
         } else {
           // Stage by stage over the block's 16 values: with one wave per
           // SIMD nothing else hides the latency of a dependent chain.
           int av[16], qv[16];
 #pragma unroll
-          for (int v = 0; v < 16; ++v) av[v] = acc_read(acc[x][y][v]);
+          for (int v = 0; v < 16; ++v) av[v] = acc_read(acc[x][4 * h + v / 4][v % 4]);
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int v = 0; v < 16; ++v) qv[v] = __double2loint(fma((double)av[v], ip, kMagic));
@@ -1017,11 +1035,11 @@ modgemm_kernel(GemmArgs g) {
 // correctly rounded to double, then ldexp by -(sftA + sftB).
 // fp64_emu_cuda/fp64_emu.cu:849-952 and the s128 helpers :53-105.
 //
-// One work group per 32x32 output block: thread t reads dword t of each
-// blocked plane (lane t/4 of the GEMM's accumulator order, elements
-// 4*(t%4) .. +3), i.e. rows 8*(t%4) + 4*(t/128) + 0..3 of column (t/4)%32 --
-// coalesced loads, 4 elements per thread, processed in lockstep so each
-// modulus constant is used four times right after its scalar load.
+// One work group per 16 x 64 output block: thread t reads dword t of each
+// blocked int8 plane and int32s 4t .. 4t+3 of each int32 plane (lane t/4 of
+// the GEMM's accumulator order, column block t%4), i.e. rows
+// 4 (t / 64) + 0..3 of column 16 (t % 4) + (t / 4) % 16 -- coalesced loads,
+// 4 elements per thread, processed in lockstep.
 
 typedef __int128 i128;
 
@@ -1059,8 +1077,8 @@ struct ReconArgs {
   const int16_t* sftB;
   const int* bits_eff;
   int64_t M, N, batch, outplane;
-  int64_t NB;          // 32-blocks per padded output row (Np / 32)
-  int64_t MBv, NBv;    // 32-blocks covering the valid M, N
+  int64_t NB;          // 64-column blocks per padded output row (Np / 64)
+  int64_t MBv, NBv;    // 16-row and 64-column blocks covering the valid M, N
   int64_t nblocks;     // batch * MBv * NBv
   int ncorr;
   int ksplit;            // S: residue / correction planes per output, summed here
@@ -1084,8 +1102,8 @@ reconstruct_kernel(ReconArgs a) {
   const int64_t rem = blk - b * per;
   const int64_t mb = rem / a.NBv, nb = rem - (rem / a.NBv) * a.NBv;
   const int l = thr >> 2, q4 = thr & 3;
-  const int64_t i0 = mb * 32 + 8 * q4 + 4 * (l >> 5);
-  const int64_t j = nb * 32 + (l & 31);
+  const int64_t i0 = mb * 16 + 4 * (l >> 4);
+  const int64_t j = nb * 64 + 16 * q4 + (l & 15);
   if (j >= a.N || i0 >= a.M) return;
 
   const int P = kP > 0 ? kP : a.tab.P;
@@ -1621,8 +1639,8 @@ int run(const Call& c) {
     ra.out = c.out + m0 * c.N;
     ra.sftA = sftA + m0; ra.sftB = sftB; ra.bits_eff = bits_eff;
     ra.M = Mc; ra.N = c.N; ra.batch = c.batch; ra.outplane = L.outplane_bytes;
-    ra.NB = L.Np / 32;
-    ra.MBv = (Mc + 31) / 32; ra.NBv = (c.N + 31) / 32;
+    ra.NB = L.Np / 64;
+    ra.MBv = (Mc + 15) / 16; ra.NBv = (c.N + 63) / 64;
     ra.nblocks = c.batch * ra.MBv * ra.NBv;
     ra.ncorr = L.ncorr;
     ra.ksplit = L.ksplit;

@@ -248,12 +248,11 @@ def sizing(ws, lay):
 
 def _plane_to_logical(raw, rows_p, depth_p):
     """One tile-blocked plane (bytes) -> int8 [rows_p, depth_p].  A 256 x 64
-    tile holds 16 fragments of 32 rows x 32 k, fragment 2*(row%256//32) +
-    (k%64)//32; inside one, lane l = 32*(k%32//16) + row%32 holds k%16 at
-    byte 16*l + k%16."""
+    tile holds 16 fragments of 16 rows x 64 k, fragment row%256//16; inside
+    one, lane l = 16*(k%64//16) + row%16 holds k%16 at byte 16*l + k%16."""
     nrt, nkt = rows_p // TILE_R, depth_p // TILE_K
-    a = raw.view(np.int8).reshape(nrt, nkt, 8, 2, 2, 32, 16)   # rt kt rb kh kc r32 kb
-    return a.transpose(0, 2, 5, 1, 3, 4, 6).reshape(rows_p, depth_p)
+    a = raw.view(np.int8).reshape(nrt, nkt, 16, 4, 16, 16)   # rt kt rb kg r16 kb
+    return a.transpose(0, 2, 4, 1, 3, 5).reshape(rows_p, depth_p)
 
 
 def planes(ws, lay, operand):
@@ -287,11 +286,12 @@ def planes(ws, lay, operand):
 
 
 def _blocks_to_logical(arr, Mp, Np):
-    """Blocked output plane -> [Mp, Np].  32x32 blocks row-block major; in a
-    block, lane l holds 16 elements, element v at (8*(v//4) + 4*(l//32) +
-    v%4, l%32), stored at 16*l + v."""
-    a = arr.reshape(Mp // 32, Np // 32, 2, 32, 4, 4)          # mb nb lh c q rr
-    return a.transpose(0, 4, 2, 5, 1, 3).reshape(Mp, Np)
+    """Blocked output plane -> [Mp, Np].  Blocks of 16 rows x 64 columns,
+    row-block major; element 16*l + 4*q + v of a block (lane l of the GEMM's
+    accumulator order, column block q, row v) is at row 4*(l//16) + v,
+    column 16*q + l%16."""
+    a = arr.reshape(Mp // 16, Np // 64, 4, 16, 4, 4)          # rb cb lh lc q v
+    return a.transpose(0, 2, 5, 1, 4, 3).reshape(Mp, Np)
 
 
 def outputs(ws, lay, primes=None):
