@@ -835,29 +835,25 @@ modgemm_kernel(GemmArgs g) {
   // Steady-state step (a copy for step kt+3 exists): an unconditional wait,
   // so the compiler's own wait tracking sees every earlier fragment read
   // retired (a conditional wait made it stall on the first read of each
-  // step), and the step in four fenced chunks, each {2 copies, then 4 times
-  // one fragment read and 4 MFMAs}: the copies reach the texture unit spread
-  // over the step instead of as a burst after the barrier, which delayed the
-  // last wave's MFMAs and made every wave wait for it at the next barrier,
-  // and each read has 4 MFMAs to land behind.
-#define FP64EMU_DMA2(kt, c)                                                                  \
-  do {                                                                                       \
-    lds_i8* st_ = (lds_i8*)(lds + ((kt) & (kStages - 1)) * kStageBytes + wave * 4096 +       \
-                            ((c) >> 1) * kTileBytes);                                        \
-    const int8_t* g_ = (((c) >> 1) ? Bt : At) + (int64_t)(kt) * kTileBytes + goff;           \
-    __builtin_amdgcn_global_load_lds(g_, st_, 16, ((c) & 1) * 2048, 0);                      \
-    __builtin_amdgcn_global_load_lds(g_, st_, 16, ((c) & 1) * 2048 + 1024, 0);               \
-  } while (0)
+  // step), and the step in four fenced chunks, each 4 times {one fragment
+  // read, 4 MFMAs} with a copy before the first and the third: the copies
+  // reach the texture unit spread over the step instead of as a burst after
+  // the barrier, which delayed the last wave's MFMAs and made every wave wait
+  // for it at the next barrier, and each read has 4 MFMAs to land behind.
   // Chunk c: MFMAs of A blocks 2c, 2c+1 against all 8 B blocks; reads of the
   // next step's fragments 4c .. 4c+3 (B 0..7, then A 0..7), so the first
   // chunk of the next step finds its operands read a step ahead.
 #define FP64EMU_CHUNK(kt, FC, FN, c, MMA)                                                    \
   do {                                                                                       \
-    FP64EMU_DMA2((kt) + 3, c);                                                               \
-    __builtin_amdgcn_sched_barrier(0);                                                       \
     const v4i* sa_ = reinterpret_cast<const v4i*>(lds + (((kt) + 1) & (kStages - 1)) * kStageBytes); \
     const v4i* sb_ = sa_ + kTileBytes / 16;                                                  \
+    lds_i8* st_ = (lds_i8*)(lds + (((kt) + 3) & (kStages - 1)) * kStageBytes + wave * 4096 + \
+                            ((c) >> 1) * kTileBytes);                                        \
+    const int8_t* g_ = (((c) >> 1) ? Bt : At) + (int64_t)((kt) + 3) * kTileBytes + goff;     \
     _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                          \
+      if (j == 0) __builtin_amdgcn_global_load_lds(g_, st_, 16, ((c) & 1) * 2048, 0);        \
+      if (j == 2) __builtin_amdgcn_global_load_lds(g_, st_, 16, ((c) & 1) * 2048 + 1024, 0); \
+      __builtin_amdgcn_sched_barrier(0);                                                     \
       const int f_ = (c) * 4 + j;                                                            \
       if (f_ < 8) FN[8 + f_] = sb_[(wn * 8 + f_) * 64 + lane];                               \
       else FN[f_ - 8] = sa_[(wm * 8 + f_ - 8) * 64 + lane];                                  \
@@ -920,7 +916,6 @@ modgemm_kernel(GemmArgs g) {
 #undef FP64EMU_READF
 #undef FP64EMU_MMA
 #undef FP64EMU_STEP
-#undef FP64EMU_DMA2
 #undef FP64EMU_CHUNK
 #undef FP64EMU_STEP_FULL
 
