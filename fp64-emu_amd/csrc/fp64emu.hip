@@ -563,7 +563,11 @@ extract_kernel(ExtractArgs a) {
   uint32_t hw[4] = {0u, 0u, 0u, 0u}, qw[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int jj = 0; jj < 16; ++jj) {
-    const double y = ldexp(fabs(x[jj]), shift);
+    // Infinities and NaNs scale to 0, as the reference's integer split of
+    // their encoding does (the shift that carries exponent 0x7FF is far past
+    // 64 bits); every finite y is below 2^53.
+    double y = ldexp(fabs(x[jj]), shift);
+    y = y <= 0x1p54 ? y : 0.0;
     const double Tu = rint(y);
     const double td = copysign(Tu, x[jj]);
     if (a.use_corr) {

@@ -180,3 +180,25 @@ def test_deep_k_moduli_orders(dev, order):
     assert lay.deep == 1
     oout, info = O.mm(A.cpu().numpy(), B.cpu().numpy(), 0, primes)
     assert bits_equal(out.cpu().numpy(), oout), "deep-K output differs from the oracle"
+
+
+def test_non_finite_entries(dev):
+    """Infinities and NaNs contribute 0, as the reference's integer split of
+    their encoding (fp64_emu_cuda/fp64_emu.cu:300-321) gives; the rows and
+    columns holding them keep the unnarrowed shift (bits - 1, fp64_emu.cu:138)
+    and fall back to the worst-case width (:213-216).  Entries here stay below
+    4 in magnitude, where the reference's 64-bit split of such rows does not
+    wrap, so every stage matches the oracle."""
+    print("case non-finite entries mm_nt 48x40x300", flush=True)
+    g = torch.Generator().manual_seed(77)
+    A = 0.5 * torch.randn((48, 300), dtype=torch.float64, generator=g)
+    B = 0.5 * torch.randn((300, 40), dtype=torch.float64, generator=g)
+    A[3, 10] = float("inf")
+    A[5, :] = float("inf")
+    A[7, 20] = float("nan")
+    A[9, 1] = float("-inf")
+    B[2, 7] = float("nan")
+    B[:, 11] = float("-inf")
+    B[40, 3] = float("inf")
+    out, _, _ = check_call("mm_nt", A.to(dev), B.to(dev), O.PRIMES[:14])
+    assert torch.isfinite(out).all()
