@@ -202,3 +202,21 @@ def test_non_finite_entries(dev):
     B[40, 3] = float("inf")
     out, _, _ = check_call("mm_nt", A.to(dev), B.to(dev), O.PRIMES[:14])
     assert torch.isfinite(out).all()
+
+
+def test_extreme_magnitudes(dev):
+    """Rows scaled by 2^±990 (shifts far outside int8 widths): products that
+    overflow to infinity or underflow to subnormals and zero after the final
+    ldexp, against the oracle bit for bit."""
+    print("case extreme magnitudes mm_nt 40x36x200", flush=True)
+    g = torch.Generator().manual_seed(88)
+    A = torch.randn((40, 200), dtype=torch.float64, generator=g)
+    B = torch.randn((200, 36), dtype=torch.float64, generator=g)
+    A[:10] *= 2.0 ** 990
+    A[10:20] *= 2.0 ** -990
+    A[20:24] *= 2.0 ** -1060            # subnormal rows
+    B[:, :9] *= 2.0 ** 990
+    B[:, 9:18] *= 2.0 ** -990
+    out, _, _ = check_call("mm_nt", A.to(dev), B.to(dev), O.PRIMES[:14])
+    o = out.cpu()
+    assert torch.isinf(o[:10, :9]).any() and (o[10:20, 9:18] == 0).any()
