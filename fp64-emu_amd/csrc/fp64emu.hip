@@ -637,7 +637,8 @@ extract_kernel(ExtractArgs a) {
 //
 // 4 waves in a 2x2 arrangement, 128x128 per wave = 8x8 v_mfma_i32_16x16x64_i8
 // tiles (256 accumulator registers; the 16x16 form draws less power per
-// operation than 32x32x32, so under the power cap the clock runs higher).  Operand tiles stream into a 4-stage LDS
+// operation than 32x32x32, so under the power cap the clock runs higher).
+// Operand tiles stream into a 4-stage LDS
 // ring with direct global->LDS copies (prefetch distance 3 k-steps); the
 // planes are stored in fragment order, so each stage is a linear copy and
 // every fragment read is 16 contiguous bytes per lane (bank-conflict free).
