@@ -220,3 +220,21 @@ def test_extreme_magnitudes(dev):
     out, _, _ = check_call("mm_nt", A.to(dev), B.to(dev), O.PRIMES[:14])
     o = out.cpu()
     assert torch.isinf(o[:10, :9]).any() and (o[10:20, 9:18] == 0).any()
+
+
+@pytest.mark.parametrize("kind,batch,M,N,K,P,exact", [
+    ("bmm", 2, 40, 30, 5000, 14, True),       # K-split with batch > 1 (split-major planes)
+    ("mm_nt", 1, 50, 60, 20000, 15, False),   # K-split, inexact combine
+    ("mm_nt", 1, 33, 20, 6000, 10, True),     # K-split, generic reconstruction (10 moduli)
+])
+def test_ksplit_variants(dev, kind, batch, M, N, K, P, exact):
+    from fp64_emu import capi
+    print(f"case K-split {kind} b={batch} {M}x{N}x{K} P={P} exact={exact}", flush=True)
+    if kind == "bmm":
+        A = _randn((batch, M, K), 300 + M, dev)
+        B = _randn((batch, N, K), 301 + N, dev)
+    else:
+        A = _randn((M, K), 300 + M, dev)
+        B = _randn((K, N), 301 + N, dev)
+    assert capi.layout(batch, M, N, K, P, True).ksplit > 1
+    check_call(kind, A, B, O.PRIMES[:P], exact=exact)
