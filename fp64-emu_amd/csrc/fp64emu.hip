@@ -264,48 +264,63 @@ __device__ __forceinline__ void row_stats_out(double m, double s2, int bits, int
   *sft = (int16_t)sh;
 }
 
+// One wave per row (four rows per block).  Lane l stands for the partial
+// sums l, l + 64, l + 128 and l + 192 of a 256-thread row pass: element c
+// goes to sum c % 256, FMA-accumulated in increasing c, and the 256 sums
+// fold by the same pairwise tree (strides 128 and 64 inside the lane, 32 .. 1
+// across lanes), so the sum of squares is the one the 256-thread form gives.
+constexpr int kRowsPerBlock = kThreads / 64;
+
+template <int kBlocks>
+__device__ __forceinline__ void row_pass(const double* __restrict__ x, int64_t c, double& mx,
+                                         double (&ss)[4]) {
+  double v[4 * kBlocks];
+#pragma unroll
+  for (int u = 0; u < 4 * kBlocks; ++u) v[u] = x[c + 64 * u];
+#pragma unroll
+  for (int u = 0; u < 4 * kBlocks; ++u) {
+    mx = fmax(mx, fabs(v[u]));
+    ss[u & 3] = fma(v[u], v[u], ss[u & 3]);
+  }
+}
+
 __global__ void __launch_bounds__(kThreads)
 size_rows_kernel(const double* __restrict__ A, int64_t rowsA, const double* __restrict__ B,
-                 int64_t K, int bits, int16_t* __restrict__ sftA, float* __restrict__ lgA,
-                 int16_t* __restrict__ sftB, float* __restrict__ lgB) {
-  const int64_t br = blockIdx.x;
-  const bool isA = br < rowsA;
-  const int64_t r = isA ? br : br - rowsA;
-  const double* __restrict__ x = (isA ? A : B) + r * K;
-  const int tid = threadIdx.x;
-  double mx = 0.0, ss = 0.0;
-  // Loads go out eight at a time; the fma chain keeps the reference's order.
-  int64_t c = tid;
-  for (; c + 7 * kThreads < K; c += 8 * kThreads) {
-    double v[8];
+                 int64_t rows, int64_t K, int bits, int16_t* __restrict__ sftA,
+                 float* __restrict__ lgA, int16_t* __restrict__ sftB, float* __restrict__ lgB) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const bool isA = row < rowsA;
+  const int64_t r = isA ? row : row - rowsA;
+  const double* __restrict__ x = (isA ? A : B) + r * K + lane;
+  double mx = 0.0, ss[4] = {0.0, 0.0, 0.0, 0.0};
+  // Sixteen loads in flight, then eight, then guarded 256-element blocks.
+  int64_t c = 0;
+  for (; c + 1024 <= K; c += 1024) row_pass<4>(x, c, mx, ss);
+  if (c + 512 <= K) {
+    row_pass<2>(x, c, mx, ss);
+    c += 512;
+  }
+  for (; c < K; c += 256) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = x[c + u * kThreads];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      mx = fmax(mx, fabs(v[u]));
-      ss = fma(v[u], v[u], ss);
+    for (int u = 0; u < 4; ++u) {
+      if (c + 64 * u + lane < K) {
+        const double v = x[c + 64 * u];
+        mx = fmax(mx, fabs(v));
+        ss[u] = fma(v, v, ss[u]);
+      }
     }
   }
-  for (; c < K; c += kThreads) {
-    const double v = x[c];
-    mx = fmax(mx, fabs(v));
-    ss = fma(v, v, ss);
-  }
-  __shared__ double smx[kThreads], sss[kThreads];
-  smx[tid] = mx;
-  sss[tid] = ss;
-  __syncthreads();
+  double t = (ss[0] + ss[2]) + (ss[1] + ss[3]);
 #pragma unroll
-  for (int s = kThreads / 2; s > 0; s >>= 1) {
-    if (tid < s) {
-      smx[tid] = fmax(smx[tid], smx[tid + s]);
-      sss[tid] = sss[tid] + sss[tid + s];
-    }
-    __syncthreads();
+  for (int s = 32; s > 0; s >>= 1) {
+    t = t + __shfl_down(t, s);
+    mx = fmax(mx, __shfl_down(mx, s));
   }
-  if (tid == 0) {
-    if (isA) row_stats_out(smx[0], sss[0], bits, &sftA[r], &lgA[r]);
-    else row_stats_out(smx[0], sss[0], bits, &sftB[r], &lgB[r]);
+  if (lane == 0) {
+    if (isA) row_stats_out(mx, t, bits, &sftA[r], &lgA[r]);
+    else row_stats_out(mx, t, bits, &sftB[r], &lgB[r]);
   }
 }
 
@@ -377,62 +392,65 @@ size_cols_final_kernel(const double* __restrict__ pmax, const double* __restrict
 }
 
 // Width pick: g = floor((log2M - 1 - (max lgA + max lgB + 0.5)) / 2),
-// g <= 53 - bits, be = max(bits + g, 16); g folded into every shift and be
-// kept on the device.  fp64_emu_cuda/fp64_emu.cu:191-231.
+// g <= 53 - bits, be = max(bits + g, 16).  bits_eff[0] = be and
+// bits_eff[1] = be - bits, the amount every per-row and per-column shift
+// grows by; the consumers add it on the fly, so the shifts are never
+// rewritten.  fp64_emu_cuda/fp64_emu.cu:191-231.
 constexpr int kPickThreads = 1024;
+
+__device__ __forceinline__ float max4(float4 v) { return fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)); }
+
+// Max of lg[0, n) in one block: eight float4 loads in flight per thread
+// (the workspace slices are 256-byte aligned), a scalar tail.
+__device__ __forceinline__ float block_max_lg(const float* __restrict__ lg, int64_t n, int tid) {
+  constexpr int T = kPickThreads;
+  const float4* __restrict__ v4 = reinterpret_cast<const float4*>(lg);
+  const int64_t n4 = n / 4;
+  float a = -INFINITY;
+  int64_t i = tid;
+  for (; i + 7 * T < n4; i += 8 * T) {
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = v4[i + u * T];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a = fmaxf(a, max4(v[u]));
+  }
+  for (; i < n4; i += T) a = fmaxf(a, max4(v4[i]));
+  if (tid < n - 4 * n4) a = fmaxf(a, lg[4 * n4 + tid]);
+  return a;
+}
 
 __global__ void __launch_bounds__(kPickThreads)
 pick_width_kernel(const float* __restrict__ lgA, int64_t m, const float* __restrict__ lgB,
-                  int64_t n, float log2M, int bits, int16_t* __restrict__ sftA,
-                  int16_t* __restrict__ sftB, int* __restrict__ bits_eff) {
+                  int64_t n, float log2M, int bits, int* __restrict__ bits_eff) {
   constexpr int T = kPickThreads;
-  __shared__ float sa[T], sb[T];
-  __shared__ int s_g;
+  __shared__ float sa[T / 64], sb[T / 64];
   const int tid = threadIdx.x;
-  float a = -INFINITY, b = -INFINITY;
-  // Eight independent loads in flight per thread (a max is order-free).
-  int64_t i = tid;
-  for (; i + 7 * T < m; i += 8 * T) {
-    float v[8];
+  float a = block_max_lg(lgA, m, tid);
+  float b = block_max_lg(lgB, n, tid);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = lgA[i + u * T];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) a = fmaxf(a, v[u]);
+  for (int s = 32; s > 0; s >>= 1) {
+    a = fmaxf(a, __shfl_down(a, s));
+    b = fmaxf(b, __shfl_down(b, s));
   }
-  for (; i < m; i += T) a = fmaxf(a, lgA[i]);
-  int64_t j = tid;
-  for (; j + 7 * T < n; j += 8 * T) {
-    float v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = lgB[j + u * T];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) b = fmaxf(b, v[u]);
+  if ((tid & 63) == 0) {
+    sa[tid >> 6] = a;
+    sb[tid >> 6] = b;
   }
-  for (; j < n; j += T) b = fmaxf(b, lgB[j]);
-  sa[tid] = a;
-  sb[tid] = b;
   __syncthreads();
-  for (int s = T / 2; s > 0; s >>= 1) {
-    if (tid < s) {
-      sa[tid] = fmaxf(sa[tid], sa[tid + s]);
-      sb[tid] = fmaxf(sb[tid], sb[tid + s]);
-    }
-    __syncthreads();
-  }
   if (tid == 0) {
-    const float need = sa[0] + sb[0] + 0.5f;
+#pragma unroll
+    for (int w = 1; w < T / 64; ++w) {
+      a = fmaxf(a, sa[w]);
+      b = fmaxf(b, sb[w]);
+    }
+    const float need = a + b + 0.5f;
     int g = 0;
     if (isfinite(need)) g = (int)floorf((log2M - 1.0f - need) * 0.5f);
     g = min(g, 53 - bits);
     const int be = max(bits + g, 16);
-    s_g = be - bits;
     bits_eff[0] = be;
-  }
-  __syncthreads();
-  const int g = s_g;
-  if (g != 0) {
-    for (int64_t q = tid; q < m; q += T) sftA[q] = (int16_t)(sftA[q] + g);
-    for (int64_t q = tid; q < n; q += T) sftB[q] = (int16_t)(sftB[q] + g);
+    bits_eff[1] = be - bits;
   }
 }
 
@@ -530,8 +548,8 @@ extract_kernel(ExtractArgs a) {
 
   // Shift: per row of A / of B [N,K]; per column of B [K,N] -- one per lane.
   const int16_t* sfts = isA ? a.sftA : a.sftB;
-  const int shift = rowok ? (int)sfts[b * R + r] : 0;
   const int be = a.bits_eff[0];
+  const int shift = rowok ? (int)sfts[b * R + r] + a.bits_eff[1] : 0;
 
   double x[16];
   if (!rowok || k0 >= K) {
@@ -1268,7 +1286,8 @@ reconstruct_kernel(ReconArgs a) {
   }
 
   const int cshift = a.bits_eff[0] - 15;
-  const int sj = (int)a.sftB[b * a.N + j];
+  // Both shifts grew by bits_eff[1] at the width pick.
+  const int sj = (int)a.sftB[b * a.N + j] + 2 * a.bits_eff[1];
   const int16_t* sA = a.sftA + b * a.M + i0;
   double* outp = a.out + (b * a.M + i0) * a.N + j;
 
@@ -1505,6 +1524,8 @@ int run(const Call& c) {
   }
   if (!c.A || !c.B) return fail(FP64EMU_EINVAL, "null operand pointer");
   if (!c.ws) return fail(FP64EMU_EWORKSPACE, "workspace too small");
+  if (reinterpret_cast<uintptr_t>(c.ws) % kAlign)
+    return fail(FP64EMU_EINVAL, "workspace must be 256-byte aligned");
   if (c.ws_bytes < L.total) {
     // Short workspace: the fewest row chunks of A that fit (batch 1, not
     // K-segmented, no phase events).
@@ -1528,7 +1549,7 @@ int run(const Call& c) {
     const int64_t limit = (int64_t)0xFFFFFFFFu / kThreads;
     const int64_t nkt_max = L.Kp / kTileK;
     const int64_t grids[4] = {
-        MF + NF,                                                   // row sizing
+        (MF + NF + kRowsPerBlock - 1) / kRowsPerBlock,             // row sizing
         c.batch * (L.chunk_rows / 64 + L.Np / 64) * nkt_max,       // extraction
         (int64_t)(c.P + L.ncorr) * c.batch * L.ksplit * (L.chunk_rows / kTileR) * (L.Np / kTileR),
         c.batch * ((c.M + 31) / 32) * ((c.N + 31) / 32)};          // reconstruction
@@ -1552,11 +1573,11 @@ int run(const Call& c) {
 
   // 1. sizing
   if (!c.b_kn) {
-    hipLaunchKernelGGL(size_rows_kernel, dim3((unsigned)(MF + NF)), dim3(kThreads), 0, s, c.A, MF,
-                       c.B, c.K, c.bits, sftA, lgA, sftB, lgB);
+    hipLaunchKernelGGL(size_rows_kernel, dim3((unsigned)((MF + NF + kRowsPerBlock - 1) / kRowsPerBlock)),
+                       dim3(kThreads), 0, s, c.A, MF, c.B, MF + NF, c.K, c.bits, sftA, lgA, sftB, lgB);
   } else {
-    hipLaunchKernelGGL(size_rows_kernel, dim3((unsigned)MF), dim3(kThreads), 0, s, c.A, MF, c.A,
-                       c.K, c.bits, sftA, lgA, sftB, lgB);
+    hipLaunchKernelGGL(size_rows_kernel, dim3((unsigned)((MF + kRowsPerBlock - 1) / kRowsPerBlock)),
+                       dim3(kThreads), 0, s, c.A, MF, c.A, MF, c.K, c.bits, sftA, lgA, sftB, lgB);
     int64_t kslab; int nslab;
     slab_split(NF, c.K, &kslab, &nslab);
     const unsigned gcx = (unsigned)((NF + kThreads - 1) / kThreads);
@@ -1567,7 +1588,7 @@ int run(const Call& c) {
                        nslab, c.bits, sftB, lgB);
   }
   hipLaunchKernelGGL(pick_width_kernel, dim3(1), dim3(kPickThreads), 0, s, lgA, MF, lgB, NF,
-                     std::min(tab.log2M, 126.0f), c.bits, sftA, sftB, bits_eff);
+                     std::min(tab.log2M, 126.0f), c.bits, bits_eff);
 
   // 2-4. Per row chunk of A (one unless the workspace is short) and per K
   // segment (one unless deep): extraction (covering the padded planes

@@ -235,14 +235,17 @@ def _ws_bytes(ws):
 
 
 def sizing(ws, lay):
-    """(sftA [batch*M], sftB [batch*N], lgA, lgB, bits_eff) after the call."""
+    """(sftA [batch*M], sftB [batch*N], lgA, lgB, bits_eff) after the call.
+    The workspace keeps the shifts as sized per row/column and, beside
+    bits_eff, the amount the width pick adds to every one of them; the
+    shifts returned here include it."""
     w = _ws_bytes(ws)
     MF, NF = lay.batch * lay.M, lay.batch * lay.N
-    sftA = w[lay.off_sftA:lay.off_sftA + 2 * MF].view(np.int16).copy()
-    sftB = w[lay.off_sftB:lay.off_sftB + 2 * NF].view(np.int16).copy()
+    be, g = (int(v) for v in w[lay.off_bits:lay.off_bits + 8].view(np.int32))
+    sftA = (w[lay.off_sftA:lay.off_sftA + 2 * MF].view(np.int16) + g).astype(np.int16)
+    sftB = (w[lay.off_sftB:lay.off_sftB + 2 * NF].view(np.int16) + g).astype(np.int16)
     lgA = w[lay.off_lgA:lay.off_lgA + 4 * MF].view(np.float32).copy()
     lgB = w[lay.off_lgB:lay.off_lgB + 4 * NF].view(np.float32).copy()
-    be = int(w[lay.off_bits:lay.off_bits + 4].view(np.int32)[0])
     return sftA, sftB, lgA, lgB, be
 
 

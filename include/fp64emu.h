@@ -5,9 +5,10 @@
  * pairwise-coprime moduli (one CDNA4 INT8-MFMA GEMM each), a first-order
  * quantization correction (hi7 x q7 cross GEMMs) and balanced-Garner
  * reconstruction.  Every entry point enqueues asynchronously on `stream`
- * and allocates nothing: the caller passes a device workspace of at least
- * fp64emu_workspace_size() bytes (the torch binding takes it from the
- * caching allocator, which keeps the call graph-capturable).  All pointers
+ * and allocates nothing: the caller passes a 256-byte aligned device
+ * workspace of at least fp64emu_workspace_size() bytes (hipMalloc and the
+ * torch caching allocator, which the binding uses and which keeps the call
+ * graph-capturable, both align that far).  All pointers
  * are device pointers unless the parameter says "host".
  *
  * Return value: 0 on success, nonzero on error; fp64emu_last_error() then

@@ -112,7 +112,7 @@ def test_layout_rejects_bad_arguments():
 
 
 def _call(kind="mm_nt", M=8, N=8, K=16, primes=None, bits=53, ws_bytes=None, null_ops=False,
-          batch=1):
+          batch=1, ws_addr=0x2000):
     """Invoke a C entry point with host-side dummies; every case here fails
     validation (or is empty) before any pointer is dereferenced or any HIP
     call is made."""
@@ -123,7 +123,7 @@ def _call(kind="mm_nt", M=8, N=8, K=16, primes=None, bits=53, ws_bytes=None, nul
     ws_size = capi.workspace_size(batch, max(M, 0), max(N, 0), max(K, 0), max(1, min(pr.size, 20)),
                                   True)
     ws_bytes = ws_size if ws_bytes is None else ws_bytes
-    ws = ctypes.c_void_p(0x2000)
+    ws = ctypes.c_void_p(ws_addr)
     if kind in ("mm", "mm_nt"):
         st = getattr(L, "fp64emu_" + kind)(dummy, dummy, dummy, M, N, K, pp, None, None, pr.size, 1,
                                            bits, 1, ws, ws_bytes, None)
@@ -151,6 +151,7 @@ def test_validation_messages(kind):
         assert _call(kind, K=128 * 65536 + 1) == (EINVAL, "K bound: 128 segments of 65536")
     assert _call(kind, M=-1) == (EINVAL, "shapes must be non-negative")
     assert _call(kind, ws_bytes=100) == (EWORKSPACE, "workspace too small")
+    assert _call(kind, ws_addr=0x2008) == (EINVAL, "workspace must be 256-byte aligned")
     assert _call(kind, null_ops=True)[0] == EINVAL
 
 
