@@ -193,6 +193,18 @@ int choose_ksplit(int64_t batch, int64_t tiles, int64_t nkt, int P, int ncorr) {
   return best;
 }
 
+// The narrow GEMM (256 x 128 tiles, two groups per CU) for products whose
+// groups are short (k-steps <= kNarrowMaxSteps; the fused correction slot
+// runs twice as many) and numerous enough to give every CU two.
+constexpr int64_t kNarrowMaxSteps = 16;
+
+bool use_narrow_gemm(const fp64emu_layout_t& L) {
+  if (L.deep || L.ksplit != 1 || L.Kp / kTileK > kNarrowMaxSteps) return false;
+  const int64_t groups = (int64_t)(L.nprimes + L.ncorr) * L.batch * (L.chunk_rows / kTileR) *
+                         ((L.N + 127) / 128);
+  return groups >= 2 * kCUs;
+}
+
 // nchunk_req > 1 (batch 1, not K-segmented): the planes of A and the output
 // planes hold one chunk of ceil(TM / nchunk_req) row tiles at a time.
 void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool corr,
@@ -246,6 +258,7 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   L->off_corr = take((L->deep ? sizeof(int64_t) : sizeof(int32_t)) *
                      (size_t)(L->ksplit * batch * L->ncorr * L->outplane_bytes));
   L->total = o;
+  L->gemm_tile_cols = use_narrow_gemm(*L) ? 128 : 256;
 }
 
 // ---------------------------------------------------------------------------
@@ -681,7 +694,8 @@ struct GemmArgs {
   int64_t outplane;    // Mp * Np
   int64_t total;       // work groups
   int nkt;             // k tiles of a residue plane
-  int TM, TN;          // 256-tiles per member
+  int TM, TN;          // output tiles per member (256 x 256, or 256 x 128 for the narrow kernel)
+  int64_t NB;          // 64-column output blocks per output row: Np / 64
   int P, ncorr, nslots, batch;
   int ksplit;          // groups per output tile, each over a contiguous K range
   int p[kMaxP];
@@ -761,14 +775,29 @@ __device__ __forceinline__ void mfma_fence() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-constexpr int kStages = 4;                   // LDS ring: 4 x 32 KiB
-constexpr int kStageBytes = 2 * kTileBytes;  // A tile then B tile
-constexpr int kDmaPerStep = 8;               // per wave: 4 KiB of A + 4 KiB of B
+// Two tile shapes.  kWN = 8: 256 x 256 output tiles, each wave 128 x 128
+// (8 x 8 accumulator quads, half the register file: one group per CU), a
+// 4-stage ring of 32 KiB.  kWN = 4: 256 x 128 tiles, each wave 128 x 64, a
+// 3-stage ring of 24 KiB, two groups per CU: for shallow products, whose
+// groups run only a few k-steps, one group's prologue and epilogue (operand
+// latency, residue stores) overlap the other's MFMAs.  Both copy stage
+// kt + 3 during k-step kt.
+template <int kWN>
+struct GemmShape {
+  static constexpr int kS = kWN == 8 ? 4 : 3;            // LDS ring stages
+  static constexpr int kBBytes = kWN * 2048;             // B tile: 32 kWN columns x 64 k
+  static constexpr int kSB = kTileBytes + kBBytes;       // stage: A tile then B tile
+  static constexpr int kDma = 4 + kWN / 2;               // copies per wave per stage
+  static constexpr int kHB = kWN / 4;                    // 64-column output blocks per wave
+  static constexpr int kCols = 32 * kWN;                 // tile columns
+};
 
-template <bool kDeep>
-__global__ void __launch_bounds__(kThreads, 1)
+template <bool kDeep, int kWN>
+__global__ void __launch_bounds__(kThreads, kWN == 8 ? 1 : 2)
 modgemm_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) int8_t lds[kStages * kStageBytes];
+  using Sh = GemmShape<kWN>;
+  constexpr int kS = Sh::kS, kSB = Sh::kSB, kDma = Sh::kDma, kHB = Sh::kHB;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[kS * kSB];
 
   // XCD-aware order: work group i runs on XCD i % 8.  Within each full chunk
   // of 256 groups, XCD x takes logical items 32x .. 32x+31, an 8x4 block of
@@ -806,50 +835,64 @@ modgemm_kernel(GemmArgs g) {
 
   const int8_t* At = g.A + b * g.memberA + (int64_t)plane * g.planeA +
                      ((int64_t)mt * rstride + kt0) * kTileBytes;
+  // A narrow column tile is one half (8 fragments) of a 256-row plane tile.
+  const int nrt = kWN == 8 ? nt : nt >> 1;
+  const int nhalf = kWN == 8 ? 0 : nt & 1;
   const int8_t* Bt = g.B + b * g.memberB + (int64_t)plane * g.planeB +
-                     ((int64_t)nt * rstride + kt0) * kTileBytes;
+                     ((int64_t)nrt * rstride + kt0) * kTileBytes + nhalf * Sh::kBBytes;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  // Each wave copies fragments 4*wave .. 4*wave+3 of both operand tiles:
-  // the instruction offset advances the global and the LDS address alike.
+  // Each wave copies fragments 4*wave .. 4*wave+3 of the A tile and
+  // kWN/2 of the B tile (2 KiB or 1 KiB blocks): the instruction offset
+  // advances the global and the LDS address alike.
   const uint32_t goff = (uint32_t)(wave * 4096 + lane * 16);
+  const uint32_t goffB = (uint32_t)(wave * (kWN / 2) * 1024 + lane * 16);
+#define FP64EMU_SLOT(kt) ((kS == 4) ? ((kt) & 3) : ((kt) % kS))
+#define FP64EMU_COPY_A(kt, j)                                                               \
+  __builtin_amdgcn_global_load_lds(At + (int64_t)(kt) * kTileBytes + goff,                  \
+                                   (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + wave * 4096),   \
+                                   16, (j) * 1024, 0)
+#define FP64EMU_COPY_B(kt, j)                                                               \
+  __builtin_amdgcn_global_load_lds(Bt + (int64_t)(kt) * kTileBytes + goffB,                 \
+                                   (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + kTileBytes +    \
+                                             wave * (kWN / 2) * 1024),                      \
+                                   16, (j) * 1024, 0)
 #define FP64EMU_ISSUE(kt)                                                              \
   do {                                                                                 \
-    lds_i8* st_ = (lds_i8*)(lds + ((kt) & (kStages - 1)) * kStageBytes + wave * 4096); \
-    const int8_t* a_ = At + (int64_t)(kt) * kTileBytes + goff;                         \
-    const int8_t* b_ = Bt + (int64_t)(kt) * kTileBytes + goff;                         \
-    __builtin_amdgcn_global_load_lds(a_, st_, 16, 0, 0);                               \
-    __builtin_amdgcn_global_load_lds(a_, st_, 16, 1024, 0);                            \
-    __builtin_amdgcn_global_load_lds(a_, st_, 16, 2048, 0);                            \
-    __builtin_amdgcn_global_load_lds(a_, st_, 16, 3072, 0);                            \
-    __builtin_amdgcn_global_load_lds(b_, st_ + kTileBytes, 16, 0, 0);                  \
-    __builtin_amdgcn_global_load_lds(b_, st_ + kTileBytes, 16, 1024, 0);               \
-    __builtin_amdgcn_global_load_lds(b_, st_ + kTileBytes, 16, 2048, 0);               \
-    __builtin_amdgcn_global_load_lds(b_, st_ + kTileBytes, 16, 3072, 0);               \
+    FP64EMU_COPY_A(kt, 0);                                                             \
+    FP64EMU_COPY_A(kt, 1);                                                             \
+    FP64EMU_COPY_A(kt, 2);                                                             \
+    FP64EMU_COPY_A(kt, 3);                                                             \
+    FP64EMU_COPY_B(kt, 0);                                                             \
+    FP64EMU_COPY_B(kt, 1);                                                             \
+    if constexpr (kWN == 8) {                                                          \
+      FP64EMU_COPY_B(kt, 2);                                                           \
+      FP64EMU_COPY_B(kt, 3);                                                           \
+    }                                                                                  \
   } while (0)
   // Fragments of one k-step: F[0..7] = A row blocks 8 wm .. 8 wm + 7 (16 rows
-  // x 64 k each), F[8..15] = the same for B.
+  // x 64 k each), F[8..8+kWN) = B column blocks kWN wn .. kWN wn + kWN - 1.
 #define FP64EMU_READF(F, kt)                                                               \
   do {                                                                                     \
-    const v4i* sa_ = reinterpret_cast<const v4i*>(lds + ((kt) & (kStages - 1)) * kStageBytes); \
+    const v4i* sa_ = reinterpret_cast<const v4i*>(lds + FP64EMU_SLOT(kt) * kSB);          \
     const v4i* sb_ = sa_ + kTileBytes / 16;                                                \
-    _Pragma("unroll") for (int y = 0; y < 8; ++y) F[8 + y] = sb_[(wn * 8 + y) * 64 + lane]; \
+    _Pragma("unroll") for (int y = 0; y < kWN; ++y) F[8 + y] = sb_[(wn * kWN + y) * 64 + lane]; \
     _Pragma("unroll") for (int x = 0; x < 8; ++x) F[x] = sa_[(wm * 8 + x) * 64 + lane];     \
   } while (0)
 #define FP64EMU_MMA(F, MMA)                                                                 \
   do {                                                                                      \
     _Pragma("unroll") for (int x = 0; x < 8; ++x)                                           \
-    _Pragma("unroll") for (int y = 0; y < 8; ++y) MMA(acc[x][y], F[x], F[8 + y]);           \
+    _Pragma("unroll") for (int y = 0; y < kWN; ++y) MMA(acc[x][y], F[x], F[8 + y]);         \
   } while (0)
   // One k-step: stage kt+1 must have landed (own copies: at most one later
   // group in flight), then the barrier makes every wave's copies visible
   // and guarantees every wave finished reading the stage refilled next.
 #define FP64EMU_STEP(kt, FC, FN, MMA)                                                    \
   do {                                                                                   \
-    if ((kt) + 3 <= nk) wait_vm_lgkm0<kDmaPerStep>(); else wait_vm_lgkm0<0>();           \
+    if ((kt) + 3 <= nk) wait_vm_lgkm0<kDma>(); else wait_vm_lgkm0<0>();                  \
     barrier_lds();                                                                       \
     if ((kt) + 3 < nk) FP64EMU_ISSUE((kt) + 3);                                          \
     FP64EMU_READF(FN, (kt) + 1);                                                         \
@@ -866,16 +909,22 @@ modgemm_kernel(GemmArgs g) {
   // Chunk c: MFMAs of A blocks 2c, 2c+1 against all 8 B blocks; reads of the
   // next step's fragments 4c .. 4c+3 (B 0..7, then A 0..7), so the first
   // chunk of the next step finds its operands read a step ahead.
+  // (kWN = 4: three reads and eight MFMAs per chunk -- B 0..3 then A 0..7 --
+  // and the six copies spread as A 0, 1 | A 2 | A 3, B 0 | B 1.)
 #define FP64EMU_CHUNK(kt, FC, FN, c, MMA)                                                    \
   do {                                                                                       \
-    const v4i* sa_ = reinterpret_cast<const v4i*>(lds + (((kt) + 1) & (kStages - 1)) * kStageBytes); \
+    if constexpr (kWN == 4) FP64EMU_CHUNK_N(kt, FC, FN, c, MMA);                             \
+    else FP64EMU_CHUNK_W(kt, FC, FN, c, MMA);                                                \
+  } while (0)
+#define FP64EMU_CHUNK_W(kt, FC, FN, c, MMA)                                                  \
+  do {                                                                                       \
+    const v4i* sa_ = reinterpret_cast<const v4i*>(lds + FP64EMU_SLOT((kt) + 1) * kSB);      \
     const v4i* sb_ = sa_ + kTileBytes / 16;                                                  \
-    lds_i8* st_ = (lds_i8*)(lds + (((kt) + 3) & (kStages - 1)) * kStageBytes + wave * 4096 + \
-                            ((c) >> 1) * kTileBytes);                                        \
-    const int8_t* g_ = (((c) >> 1) ? Bt : At) + (int64_t)((kt) + 3) * kTileBytes + goff;     \
     _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                          \
-      if (j == 0) __builtin_amdgcn_global_load_lds(g_, st_, 16, ((c) & 1) * 2048, 0);        \
-      if (j == 2) __builtin_amdgcn_global_load_lds(g_, st_, 16, ((c) & 1) * 2048 + 1024, 0); \
+      if (j == 0 && ((c) >> 1) == 0) FP64EMU_COPY_A((kt) + 3, ((c) & 1) * 2);                \
+      if (j == 2 && ((c) >> 1) == 0) FP64EMU_COPY_A((kt) + 3, ((c) & 1) * 2 + 1);            \
+      if (j == 0 && ((c) >> 1) == 1) FP64EMU_COPY_B((kt) + 3, ((c) & 1) * 2);                \
+      if (j == 2 && ((c) >> 1) == 1) FP64EMU_COPY_B((kt) + 3, ((c) & 1) * 2 + 1);            \
       __builtin_amdgcn_sched_barrier(0);                                                     \
       const int f_ = (c) * 4 + j;                                                            \
       if (f_ < 8) FN[8 + f_] = sb_[(wn * 8 + f_) * 64 + lane];                               \
@@ -888,9 +937,33 @@ modgemm_kernel(GemmArgs g) {
       __builtin_amdgcn_sched_barrier(0);                                                     \
     }                                                                                        \
   } while (0)
+#define FP64EMU_CHUNK_N(kt, FC, FN, c, MMA)                                                  \
+  do {                                                                                       \
+    const v4i* sa_ = reinterpret_cast<const v4i*>(lds + FP64EMU_SLOT((kt) + 1) * kSB);      \
+    const v4i* sb_ = sa_ + kTileBytes / 16;                                                  \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                          \
+      if (j == 0 && (c) <= 1) FP64EMU_COPY_A((kt) + 3, (c) * 2);                             \
+      if (j == 2 && (c) == 0) FP64EMU_COPY_A((kt) + 3, 1);                                   \
+      if (j == 0 && (c) == 2) FP64EMU_COPY_A((kt) + 3, 3);                                   \
+      if (j == 2 && (c) == 2) FP64EMU_COPY_B((kt) + 3, 0);                                   \
+      if (j == 0 && (c) == 3) FP64EMU_COPY_B((kt) + 3, 1);                                   \
+      __builtin_amdgcn_sched_barrier(0);                                                     \
+      if (j < 3) {                                                                           \
+        const int f_ = (c) * 3 + j;                                                          \
+        if (f_ < 4) FN[8 + f_] = sb_[(wn * 4 + f_) * 64 + lane];                             \
+        else FN[f_ - 4] = sa_[(wm * 8 + f_ - 4) * 64 + lane];                                \
+      }                                                                                      \
+      __builtin_amdgcn_sched_barrier(0);                                                     \
+      _Pragma("unroll") for (int u = 0; u < 2; ++u) {                                        \
+        const int m_ = 2 * j + u, x = (c) * 2 + m_ / 4, y = m_ % 4;                          \
+        MMA(acc[x][y], FC[x], FC[8 + y]);                                                    \
+      }                                                                                      \
+      __builtin_amdgcn_sched_barrier(0);                                                     \
+    }                                                                                        \
+  } while (0)
 #define FP64EMU_STEP_FULL(kt, FC, FN, MMA)                                                   \
   do {                                                                                       \
-    wait_vm_lgkm0<kDmaPerStep>();                                                            \
+    wait_vm_lgkm0<kDma>();                                                                   \
     barrier_lds();                                                                           \
     FP64EMU_CHUNK(kt, FC, FN, 0, MMA);                                                       \
     FP64EMU_CHUNK(kt, FC, FN, 1, MMA);                                                       \
@@ -898,18 +971,18 @@ modgemm_kernel(GemmArgs g) {
     FP64EMU_CHUNK(kt, FC, FN, 3, MMA);                                                       \
   } while (0)
 
-  v4i acc[8][8];
+  v4i acc[8][kWN];
   if (nk == 0) {
     // A trailing K-split group past the end: its outputs are zeros.
 #pragma unroll
     for (int x = 0; x < 8; ++x)
 #pragma unroll
-      for (int y = 0; y < 8; ++y) acc[x][y] = v4i{0, 0, 0, 0};
+      for (int y = 0; y < kWN; ++y) acc[x][y] = v4i{0, 0, 0, 0};
   } else {
 #pragma unroll
-    for (int s = 0; s < kStages - 1; ++s)
+    for (int s = 0; s < 3; ++s)
       if (s < nk) FP64EMU_ISSUE(s);
-    v4i F0[16], F1[16];
+    v4i F0[8 + kWN], F1[8 + kWN];
     wait_vm_lgkm0<0>();
     barrier_lds();
     FP64EMU_READF(F0, 0);
@@ -940,14 +1013,19 @@ modgemm_kernel(GemmArgs g) {
 #undef FP64EMU_MMA
 #undef FP64EMU_STEP
 #undef FP64EMU_CHUNK
+#undef FP64EMU_CHUNK_W
+#undef FP64EMU_CHUNK_N
 #undef FP64EMU_STEP_FULL
+#undef FP64EMU_COPY_A
+#undef FP64EMU_COPY_B
+#undef FP64EMU_SLOT
 
-  // Epilogue: output blocks of 16 rows x 64 columns; this wave's 128 x 128
-  // holds 8 row blocks x 2 column blocks.  Element 16 l + 4 q + v of a
-  // block is lane l's value v of accumulator column block q (row
+  // Epilogue: output blocks of 16 rows x 64 columns; this wave's 128 x
+  // 16 kWN holds 8 row blocks x kWN/4 column blocks.  Element 16 l + 4 q + v
+  // of a block is lane l's value v of accumulator column block q (row
   // 4 (l / 16) + v, column 16 q + l % 16).
-  const int64_t NB = (int64_t)g.TN * 4;                 // 64-column blocks per output row
-  const int64_t rb0 = (int64_t)mt * 16 + wm * 8, cb0 = (int64_t)nt * 4 + wn * 2;
+  const int64_t NB = g.NB;
+  const int64_t rb0 = (int64_t)mt * 16 + wm * 8, cb0 = (int64_t)nt * (kWN / 2) + wn * kHB;
   if (kDeep && is_corr) {
     // K-segmented: this segment's correction products join the int64 sum.
     typedef long long v2l __attribute__((ext_vector_type(2)));
@@ -955,7 +1033,7 @@ modgemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int x = 0; x < 8; ++x)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < kHB; ++h) {
         v2l* d = reinterpret_cast<v2l*>(dst + ((rb0 + x) * NB + cb0 + h) * 1024 + lane * 16);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -980,7 +1058,7 @@ modgemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int x = 0; x < 8; ++x)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < kHB; ++h) {
         v4i* d = reinterpret_cast<v4i*>(dst + ((rb0 + x) * NB + cb0 + h) * 1024 + lane * 16);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -1013,7 +1091,7 @@ modgemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int x = 0; x < 8; ++x)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < kHB; ++h) {
         const int64_t blk = ((rb0 + x) * NB + cb0 + h) * 1024 + lane * 16;
         if (is_corr) {
           v4i* d = reinterpret_cast<v4i*>(cdst + blk);
@@ -1551,7 +1629,7 @@ int run(const Call& c) {
     const int64_t grids[4] = {
         (MF + NF + kRowsPerBlock - 1) / kRowsPerBlock,             // row sizing
         c.batch * (L.chunk_rows / 64 + L.Np / 64) * nkt_max,       // extraction
-        (int64_t)(c.P + L.ncorr) * c.batch * L.ksplit * (L.chunk_rows / kTileR) * (L.Np / kTileR),
+        (int64_t)(c.P + L.ncorr) * c.batch * L.ksplit * (L.chunk_rows / kTileR) * (L.Np / 128),
         c.batch * ((c.M + 31) / 32) * ((c.N + 31) / 32)};          // reconstruction
     for (int64_t gsz : grids)
       if (gsz > limit) return fail(FP64EMU_EINVAL, "problem too large for one launch");
@@ -1601,7 +1679,12 @@ int run(const Call& c) {
   ga.memberA = L.memberA_bytes; ga.memberB = L.memberB_bytes;
   ga.planeA = L.planeA_bytes; ga.planeB = L.planeB_bytes;
   ga.outplane = L.outplane_bytes;
-  ga.TM = (int)(L.chunk_rows / kTileR); ga.TN = (int)(L.Np / kTileR);
+  // Shallow products with many groups run the narrow kernel (two groups per
+  // CU); its column tiles past N hold only padding and are not launched.
+  const bool narrow = L.gemm_tile_cols == 128;
+  ga.TM = (int)(L.chunk_rows / kTileR);
+  ga.TN = narrow ? (int)((c.N + 127) / 128) : (int)(L.Np / kTileR);
+  ga.NB = L.Np / 64;
   ga.P = c.P; ga.ncorr = L.ncorr; ga.nslots = c.P + L.ncorr; ga.batch = (int)c.batch;
   ga.ksplit = L.ksplit;
   for (int t = 0; t < kMaxP; ++t) { ga.p[t] = tab.p[t]; ga.invp[t] = tab.invp[t]; }
@@ -1636,9 +1719,11 @@ int run(const Call& c) {
       ga.nkt = (int)nkt;
       ga.first = seg == 0 ? 1 : 0;
       if (L.deep)
-        hipLaunchKernelGGL(modgemm_kernel<true>, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+        hipLaunchKernelGGL((modgemm_kernel<true, 8>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+      else if (narrow)
+        hipLaunchKernelGGL((modgemm_kernel<false, 4>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       else
-        hipLaunchKernelGGL(modgemm_kernel<false>, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+        hipLaunchKernelGGL((modgemm_kernel<false, 8>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       for (int t = 0; t < c.P && !L.deep; ++t) {
         if ((tab.p[t] & 1) || tab.p[t] == 256) continue;
         const int64_t np = (int64_t)L.ksplit * c.batch;

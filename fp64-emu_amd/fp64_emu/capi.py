@@ -37,7 +37,8 @@ class Layout(ctypes.Structure):
                 ("memberB_bytes", ctypes.c_int64), ("outplane_bytes", ctypes.c_int64)] + [
                    (n, ctypes.c_size_t) for n in (
                        "off_sftA", "off_sftB", "off_lgA", "off_lgB", "off_bits", "off_pmax",
-                       "off_pss", "off_planesA", "off_planesB", "off_res8", "off_corr", "total")]
+                       "off_pss", "off_planesA", "off_planesB", "off_res8", "off_corr", "total")] + [
+                   ("gemm_tile_cols", ctypes.c_int)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}

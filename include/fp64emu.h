@@ -153,6 +153,8 @@ typedef struct {
                                planes (deep: one int64 sum plane) */
   size_t off_sftA, off_sftB, off_lgA, off_lgB, off_bits, off_pmax, off_pss;
   size_t off_planesA, off_planesB, off_res8, off_corr, total;
+  int gemm_tile_cols;       /* columns of one modular-GEMM output tile: 256, or 128 for
+                               shallow products with many tiles (two work groups per CU) */
 } fp64emu_layout_t;
 
 int fp64emu_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int nprimes, int use_corr,

@@ -238,3 +238,31 @@ def test_ksplit_variants(dev, kind, batch, M, N, K, P, exact):
         B = _randn((K, N), 301 + N, dev)
     assert capi.layout(batch, M, N, K, P, True).ksplit > 1
     check_call(kind, A, B, O.PRIMES[:P], exact=exact)
+
+
+NARROW_CASES = [
+    # kind, batch, M, N, K, moduli, corr -- k-steps per residue group in the comment
+    ("bmm_nt", 40, 100, 100, 64, O.PRIMES[:14], True),     # 1 (corr 2), one column tile
+    ("bmm", 6, 300, 260, 200, O.PRIMES[:14], True),        # 4 (corr 8), three column tiles
+    ("bmm", 8, 260, 300, 1000, O.PRIMES[:14], True),       # 16 (corr 32), steady loop
+    ("mm_nt", 1, 1536, 1100, 700, O.PRIMES[:15], True),    # 11, odd step count
+    ("bmm_nt", 20, 256, 256, 320, O.PRIMES[:13], False),   # 5, no correction
+    ("bmm", 40, 64, 64, 128, MODULI_ORDERS[1], True),      # 2, even modulus 254 (tie fix)
+]
+
+
+@pytest.mark.parametrize("kind,batch,M,N,K,primes,corr", NARROW_CASES)
+def test_narrow_tile_parity(dev, kind, batch, M, N, K, primes, corr):
+    """Shallow products with many output tiles run the 256 x 128-tile GEMM
+    (two work groups per CU): every stage against the oracle."""
+    from fp64_emu import capi
+    print(f"case narrow GEMM {kind} b={batch} {M}x{N}x{K} P={len(primes)} corr={corr}", flush=True)
+    assert capi.layout(batch, M, N, K, len(primes), corr).gemm_tile_cols == 128
+    seed = 700 + batch + M + N + K
+    if kind in ("bmm", "bmm_nt"):
+        A = _randn((batch, M, K), seed, dev)
+        B = _randn((batch, K, N) if kind == "bmm_nt" else (batch, N, K), seed + 1, dev)
+    else:
+        A = _randn((M, K), seed, dev)
+        B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
+    check_call(kind, A, B, primes, use_corr=corr)
