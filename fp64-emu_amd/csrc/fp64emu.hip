@@ -76,7 +76,7 @@ struct ModTables {
   int nmp[kMaxP * kGarnerWords];   // balanced int8 (-M_u mod p_t) for u < t, 4 per word
   long long m64[2];                // prod of moduli 0..6 and 7..13 (1 if empty)
   double invp[kMaxP];              // RN(1 / p)
-  double c27[kMaxP];               // 2^27 mod p
+  int c31[kMaxP];                  // 2^31 mod p, balanced: |c31| <= p / 2
   float log2M;                     // float sum of (float)log2(p), as the reference
 };
 
@@ -147,7 +147,8 @@ ModTables make_tables(const int32_t* primes, int P) {
     T.p[t] = G.p[t];
     T.minv[t] = G.minv[t];
     T.invp[t] = G.invp[t];
-    T.c27[t] = (double)((1LL << 27) % primes[t]);
+    const int c31 = (int)((1LL << 31) % primes[t]);
+    T.c31[t] = 2 * c31 > primes[t] ? c31 - primes[t] : c31;
     for (int g = 0; g < kGarnerWords; ++g) T.nmp[t * kGarnerWords + g] = G.nmp[t * kGarnerWords + g];
     l2 += (float)std::log2((double)primes[t]);
   }
@@ -488,6 +489,23 @@ pick_width_kernel(const float* __restrict__ lgA, int64_t m, const float* __restr
 // plane: A = [hi7 | q7], B = [q7 | hi7], so one GEMM accumulates
 // hi7_A q7_B^T + q7_A hi7_B^T.
 
+// Balanced residue of an int32: acc - q p with q the nearest integer to
+// acc RN(1/p), read off the low word of fma(acc, RN(1/p), kMagic) (the sum's
+// mantissa holds 2^51 + q); exact while |q| < 2^23, for the 24-bit
+// multiply-add.  A modular-GEMM group of klen <= 131071 k-terms of balanced
+// residues gives |acc| <= klen p^2/4, so |q| <= klen p/4 + 1 < 2^23.
+__device__ __forceinline__ int acc_residue(int acc, double ip, int negp) {
+  const int q = __double2loint(fma((double)acc, ip, kMagic));
+  return __mul24(q, negp) + acc;
+}
+
+// Low bytes of four ints, packed little-endian into one dword.
+__device__ __forceinline__ uint32_t pack_bytes(int r0, int r1, int r2, int r3) {
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)r1, (uint32_t)r0, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)r3, (uint32_t)r2, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
 struct ExtractArgs {
   const double* A;
   const double* B;
@@ -588,9 +606,10 @@ extract_kernel(ExtractArgs a) {
   // rounds to a subnormal far below 1/2, whose rounding is then 0 anyway),
   // Tu = RNE(y) is the integer-only RNE of the reference, d = y - Tu is exact
   // (|d| <= 1/2), and RNE(256 y) - 256 Tu = RNE(256 d) because 256 Tu is even,
-  // so the tie parity is unchanged.  td = +-Tu splits as th 2^27 + tl with
-  // th = floor(td / 2^27) and tl in [0, 2^27), both exact.
-  double th[16], tl[16];
+  // so the tie parity is unchanged.  td = +-Tu (|td| <= 2^53) splits as
+  // th 2^31 + tl with th = RNE(td / 2^31), |th| <= 2^22, and |tl| <= 2^30,
+  // both exact int32s.
+  int th[16], tl[16];
   uint32_t hw[4] = {0u, 0u, 0u, 0u}, qw[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int jj = 0; jj < 16; ++jj) {
@@ -610,41 +629,56 @@ extract_kernel(ExtractArgs a) {
       hw[jj >> 2] |= ((uint32_t)hs & 0xFFu) << (8 * (jj & 3));
       qw[jj >> 2] |= ((uint32_t)qs & 0xFFu) << (8 * (jj & 3));
     }
-    const double hi = floor(ldexp(td, -27));
-    th[jj] = hi;
-    tl[jj] = fma(-hi, 134217728.0, td);            // in [0, 2^27)
+    const double hi = rint(ldexp(td, -31));
+    th[jj] = (int)hi;
+    tl[jj] = (int)fma(-hi, 2147483648.0, td);      // in [-2^30, 2^30]
   }
 
   // One plane at a time: 16 residues -> one 16-byte chunk per lane, 1 KiB
-  // contiguous per wave.
-  // rr = v - p RNE(v/p) lies in [-p/2, p/2]: balanced for odd p, and for
-  // p = 256 the byte of +128 is that of -128.  Another even p turns a tie's
-  // +p/2 into barrett_bal32's -p/2 (a separate copy of the loop, so the
-  // usual moduli carry no extra compare).
-  auto plane_residues = [&](auto tie_fix, int pi) {
-    const int pt = a.tab.p[pi];
-    const double pd = (double)pt, ip = a.tab.invp[pi], c27 = a.tab.c27[pi];
+  // contiguous per wave.  v = th (2^31 mod p) + tl is an exact int32
+  // (|v| <= 2^21 p + 2^30 < 2^31) congruent to td; its balanced residue
+  // v - p RNE(v / p) lies in [-p/2, p/2] (for odd p the quotient v RN(1/p) is
+  // at most 2^-30 off v / p, which never comes within 1/(2p) of a
+  // half-integer; 1/256 is exact; for p = 256 a residue +128 has the byte of
+  // -128).  For p >= 171 the quotient stays below 2^23 and the residue is
+  // acc_residue's one fma and two 24-bit multiply-adds; smaller moduli (only
+  // in a caller's own list) take the quotient in fp64.  Another even p turns
+  // a tie's +p/2 into barrett_bal32's -p/2.  Each variant is its own copy
+  // of the loop, so the usual moduli carry no extra compare.
+  auto plane_residues = [&](auto int_path, auto tie_fix, int pi) {
+    const int pt = a.tab.p[pi], c31 = a.tab.c31[pi];
+    const double ip = a.tab.invp[pi];
     uint32_t w4[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      uint32_t w = 0u;
+      int r[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const double v = fma(th[4 * g + u], c27, tl[4 * g + u]);
-        const double q = fma(v, ip, kMagic) - kMagic;
-        int rr = (int)fma(-q, pd, v);
-        if (decltype(tie_fix)::value) rr = rr == (pt >> 1) ? -(pt >> 1) : rr;
-        w |= ((uint32_t)rr & 0xFFu) << (8 * u);
+        const int v = __mul24(th[4 * g + u], c31) + tl[4 * g + u];
+        if (decltype(int_path)::value) {
+          r[u] = acc_residue(v, ip, -pt);
+        } else {
+          const double vd = (double)v;
+          const double q = fma(vd, ip, kMagic) - kMagic;
+          r[u] = (int)fma(-q, (double)pt, vd);
+        }
+        if (decltype(tie_fix)::value) r[u] = r[u] == (pt >> 1) ? -(pt >> 1) : r[u];
       }
-      w4[g] = w;
+      w4[g] = pack_bytes(r[0], r[1], r[2], r[3]);
     }
     *reinterpret_cast<v4i*>(base + pi * plane + off) =
         v4i{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
   };
   for (int pi = 0; pi < P; ++pi) {
     const int pt = a.tab.p[pi];
-    if ((pt & 1) || pt == 256) plane_residues(std::false_type{}, pi);
-    else plane_residues(std::true_type{}, pi);
+    const bool tie = !(pt & 1) && pt != 256;
+    if (pt >= 171) {
+      if (!tie) plane_residues(std::true_type{}, std::false_type{}, pi);
+      else plane_residues(std::true_type{}, std::true_type{}, pi);
+    } else {
+      if (!tie) plane_residues(std::false_type{}, std::false_type{}, pi);
+      else plane_residues(std::false_type{}, std::true_type{}, pi);
+    }
   }
   if (a.use_corr) {
     // Correction plane: row tile stride 2*nkt tiles; A = [hi | q], B = [q | hi].
@@ -732,23 +766,6 @@ __device__ __forceinline__ int acc_read(int a) {
   int v;
   asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
   return v;
-}
-
-// Balanced residue of one int32 modular-GEMM accumulator: acc - q p with q the
-// nearest integer to acc RN(1/p), read off the low word of
-// fma(acc, RN(1/p), kMagic) (the sum's mantissa holds 2^51 + q).  A group of
-// klen <= 131071 k-terms of balanced residues gives |acc| <= klen p^2/4, so
-// |q| <= klen p/4 + 1 < 2^23 and the 24-bit multiply-add is exact.
-__device__ __forceinline__ int acc_residue(int acc, double ip, int negp) {
-  const int q = __double2loint(fma((double)acc, ip, kMagic));
-  return __mul24(q, negp) + acc;
-}
-
-// Low bytes of four ints, packed little-endian into one dword.
-__device__ __forceinline__ uint32_t pack_bytes(int r0, int r1, int r2, int r3) {
-  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)r1, (uint32_t)r0, 0x0c0c0400u);
-  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)r3, (uint32_t)r2, 0x0c0c0400u);
-  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 // One v_mfma_i32_16x16x64_i8 accumulating in place.  Inline assembly ties
