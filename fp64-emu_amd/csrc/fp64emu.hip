@@ -73,7 +73,8 @@ struct ModTables {
   int P;
   int p[kMaxP];
   int minv[kMaxP];                 // (M_t mod p_t)^-1 mod p_t, M_t = prod_{u<t} p_u
-  int nmp[kMaxP * kGarnerWords];   // balanced int8 (-M_u mod p_t) for u < t, 4 per word
+  int mib[kMaxP];                  // minv, balanced
+  int nmp[kMaxP * kGarnerWords];   // balanced int8 (-M_u minv_t mod p_t) for u < t, 4 per word
   long long m64[2];                // prod of moduli 0..6 and 7..13 (1 if empty)
   double invp[kMaxP];              // RN(1 / p)
   int c31[kMaxP];                  // 2^31 mod p, balanced: |c31| <= p / 2
@@ -96,7 +97,10 @@ __host__ __device__ constexpr int inv_mod(int a, int m) {
 struct GarnerTab {
   int p[kMaxP];
   int minv[kMaxP];                 // (M_t mod p_t)^-1 mod p_t, M_t = prod_{u<t} p_u
-  int nmp[kMaxP * kGarnerWords];   // balanced int8 (-M_u mod p_t) for u < t, 4 per word
+  // Balanced int8 factors of digit t, 4 per word: byte u < t holds
+  // -M_u minv_t mod p_t.
+  int nmp[kMaxP * kGarnerWords];
+  int mib[kMaxP];                  // minv_t, balanced (an int8)
   double invp[kMaxP];              // RN(1 / p)
 };
 
@@ -106,14 +110,21 @@ __host__ __device__ constexpr GarnerTab garner_tables(const int* primes, int P) 
     const int pt = primes[t];
     T.p[t] = pt;
     T.invp[t] = 1.0 / (double)pt;
-    long long Mu = 1 % pt;         // M_u mod p_t, running over u
-    for (int u = 0; u < t; ++u) {
-      int bal = (int)((pt - Mu) % pt);   // -M_u mod p_t, balanced
+    long long Mt = 1 % pt;         // M_t mod p_t
+    for (int u = 0; u < t; ++u) Mt = (Mt * (primes[u] % pt)) % pt;
+    const int mi = inv_mod((int)Mt, pt);
+    T.minv[t] = mi;
+    auto put = [&](int u, long long v) {   // v in [0, p_t): balanced byte u
+      int bal = (int)v;
       if (bal > (pt - 1) / 2) bal -= pt;
       T.nmp[t * kGarnerWords + (u >> 2)] |= (int)((uint32_t)(uint8_t)(int8_t)bal << (8 * (u & 3)));
+    };
+    long long Mu = 1 % pt;         // M_u mod p_t, running over u
+    for (int u = 0; u < t; ++u) {
+      put(u, ((pt - Mu) % pt) * mi % pt);
       Mu = (Mu * (primes[u] % pt)) % pt;
     }
-    T.minv[t] = inv_mod((int)Mu, pt);
+    T.mib[t] = 2 * mi > pt ? mi - pt : mi;
   }
   return T;
 }
@@ -146,6 +157,7 @@ ModTables make_tables(const int32_t* primes, int P) {
   for (int t = 0; t < P; ++t) {
     T.p[t] = G.p[t];
     T.minv[t] = G.minv[t];
+    T.mib[t] = G.mib[t];
     T.invp[t] = G.invp[t];
     const int c31 = (int)((1LL << 31) % primes[t]);
     T.c31[t] = 2 * c31 > primes[t] ? c31 - primes[t] : c31;
@@ -497,6 +509,15 @@ pick_width_kernel(const float* __restrict__ lgA, int64_t m, const float* __restr
 __device__ __forceinline__ int acc_residue(int acc, double ip, int negp) {
   const int q = __double2loint(fma((double)acc, ip, kMagic));
   return __mul24(q, negp) + acc;
+}
+
+// sdot4 of two packed int8 words with a zero accumulator, in the VOP3P form
+// (the builtin with a constant accumulator becomes a move and the in-place
+// VOP2 form).
+__device__ __forceinline__ int sdot4_zero(uint32_t a, uint32_t b) {
+  int r;
+  asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "s"(b));
+  return r;
 }
 
 // Low bytes of four ints, packed little-endian into one dword.
@@ -1316,9 +1337,9 @@ reconstruct_kernel(ReconArgs a) {
   // the specialised kernels (no scalar registers held across the kernel),
   // kernel arguments otherwise.
   auto tab_p = [&](int t) { return kUsual ? kDefaultTab.p[t] : a.tab.p[t]; };
-  auto tab_minv = [&](int t) { return kUsual ? kDefaultTab.minv[t] : a.tab.minv[t]; };
   auto tab_invp = [&](int t) { return kUsual ? kDefaultTab.invp[t] : a.tab.invp[t]; };
   auto tab_nmp = [&](int i) { return kUsual ? kDefaultTab.nmp[i] : a.tab.nmp[i]; };
+  auto tab_mib = [&](int t) { return kUsual ? kDefaultTab.mib[t] : a.tab.mib[t]; };
 
   // Garner digits, 4 elements in lockstep.
   int dg[4][kMaxP];
@@ -1350,32 +1371,30 @@ reconstruct_kernel(ReconArgs a) {
       }
       continue;
     }
-    const int mi = tab_minv(t);
     const double nip = -tab_invp(t);
     int nmw[kGarnerWords];
 #pragma unroll
     for (int g = 0; g < kGarnerWords; ++g) nmw[g] = (4 * g < t) ? tab_nmp(t * kGarnerWords + g) : 0;
+    const int mib = tab_mib(t);
+    const int sh = 8 * (t & 3);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      // x = r_t - sum_{u<t} d_u (M_u mod p_t), seeded with r_t (|x| < 2^19).
-      int x = (int)(int8_t)(uint8_t)(w[t] >> (8 * e));
+      // y = (r_t - sum_{u<t} d_u M_u) minv_t mod p_t as dot products: r_t
+      // minv_t from byte e of the residue word (the factor word holds minv_t
+      // at byte e only), then the digits' terms; |y| < 20 * 2^14.
+      int y = sdot4_zero(w[t], (uint32_t)(uint8_t)(int8_t)mib << (8 * e));
 #pragma unroll
       for (int g = 0; g < kGarnerWords; ++g)
-        if (4 * g < t) x = __builtin_amdgcn_sdot4(dp[e][g], nmw[g], x, false);
-      const int y = __mul24(x, mi);                       // |y| < 2^27, 24-bit operands
+        if (4 * g < t) y = __builtin_amdgcn_sdot4(dp[e][g], nmw[g], y, false);
       // d = y - p q, q the nearest integer to y/p (-q is the low word of the
-      // fma rounding -y/p; |q| < 2^20).  Odd p has no ties: d lies in
+      // fma rounding -y/p; |q| < 2^19).  Odd p has no ties: d lies in
       // [-(p-1)/2, (p-1)/2].  Even p may give +p/2, barrett_bal32's -p/2.
       int d = __mul24(__double2loint(fma((double)y, nip, kMagic)), pt) + y;
       if (!kUsual && !(pt & 1)) d = d == (pt >> 1) ? -(pt >> 1) : d;
       dg[e][t] = d;
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int sh = 8 * (t & 3);
       // Insert the digit's low byte at byte t % 4 of its word.
-      dp[e][t >> 2] = (t & 3) == 0 ? dg[e][t]
-                                   : (int)__builtin_amdgcn_perm((uint32_t)dg[e][t], (uint32_t)dp[e][t >> 2],
+      dp[e][t >> 2] = (t & 3) == 0 ? d
+                                   : (int)__builtin_amdgcn_perm((uint32_t)d, (uint32_t)dp[e][t >> 2],
                                                                  (0x03020100u & ~(0xFFu << sh)) | (0x04u << sh));
     }
   }
