@@ -72,8 +72,7 @@ int fail(int code, const std::string& msg) {
 struct ModTables {
   int P;
   int p[kMaxP];
-  int minv[kMaxP];                 // (M_t mod p_t)^-1 mod p_t, M_t = prod_{u<t} p_u
-  int mib[kMaxP];                  // minv, balanced
+  int mib[kMaxP];                  // (M_t mod p_t)^-1 mod p_t, M_t = prod_{u<t} p_u, balanced
   int nmp[kMaxP * kGarnerWords];   // balanced int8 (-M_u minv_t mod p_t) for u < t, 4 per word
   long long m64[2];                // prod of moduli 0..6 and 7..13 (1 if empty)
   double invp[kMaxP];              // RN(1 / p)
@@ -96,11 +95,11 @@ __host__ __device__ constexpr int inv_mod(int a, int m) {
 // p_0 .. p_t, so the table of a modulus list serves every prefix of it.
 struct GarnerTab {
   int p[kMaxP];
-  int minv[kMaxP];                 // (M_t mod p_t)^-1 mod p_t, M_t = prod_{u<t} p_u
   // Balanced int8 factors of digit t, 4 per word: byte u < t holds
   // -M_u minv_t mod p_t.
   int nmp[kMaxP * kGarnerWords];
-  int mib[kMaxP];                  // minv_t, balanced (an int8)
+  int mib[kMaxP];                  // minv_t = (M_t mod p_t)^-1 mod p_t, M_t = prod_{u<t} p_u,
+                                   // balanced (an int8)
   double invp[kMaxP];              // RN(1 / p)
 };
 
@@ -113,7 +112,6 @@ __host__ __device__ constexpr GarnerTab garner_tables(const int* primes, int P) 
     long long Mt = 1 % pt;         // M_t mod p_t
     for (int u = 0; u < t; ++u) Mt = (Mt * (primes[u] % pt)) % pt;
     const int mi = inv_mod((int)Mt, pt);
-    T.minv[t] = mi;
     auto put = [&](int u, long long v) {   // v in [0, p_t): balanced byte u
       int bal = (int)v;
       if (bal > (pt - 1) / 2) bal -= pt;
@@ -156,7 +154,6 @@ ModTables make_tables(const int32_t* primes, int P) {
   float l2 = 0.0f;
   for (int t = 0; t < P; ++t) {
     T.p[t] = G.p[t];
-    T.minv[t] = G.minv[t];
     T.mib[t] = G.mib[t];
     T.invp[t] = G.invp[t];
     const int c31 = (int)((1LL << 31) % primes[t]);
