@@ -91,7 +91,7 @@ __host__ __device__ constexpr int inv_mod(int a, int m) {
   return ((s0 % m) + m) % m;
 }
 
-// The reconstruction's per-modulus constants.  Entry t depends only on
+// Per-modulus constants of the extraction and the reconstruction.  Entry t depends only on
 // p_0 .. p_t, so the table of a modulus list serves every prefix of it.
 struct GarnerTab {
   int p[kMaxP];
@@ -101,6 +101,7 @@ struct GarnerTab {
   int mib[kMaxP];                  // minv_t = (M_t mod p_t)^-1 mod p_t, M_t = prod_{u<t} p_u,
                                    // balanced (an int8)
   double invp[kMaxP];              // RN(1 / p)
+  int c31[kMaxP];                  // 2^31 mod p, balanced (the extraction's limb factor)
 };
 
 __host__ __device__ constexpr GarnerTab garner_tables(const int* primes, int P) {
@@ -123,6 +124,8 @@ __host__ __device__ constexpr GarnerTab garner_tables(const int* primes, int P) 
       Mu = (Mu * (primes[u] % pt)) % pt;
     }
     T.mib[t] = 2 * mi > pt ? mi - pt : mi;
+    const int c31 = (int)((1LL << 31) % pt);
+    T.c31[t] = 2 * c31 > pt ? c31 - pt : c31;
   }
   return T;
 }
@@ -133,6 +136,16 @@ __host__ __device__ constexpr GarnerTab garner_tables(const int* primes, int P) 
 constexpr int kDefaultModuli[kMaxP] = {256, 255, 253, 251, 247, 241, 239, 233, 229, 227,
                                        223, 217, 211, 199, 197, 193, 191, 181, 179, 173};
 __device__ constexpr GarnerTab kDefaultTab = garner_tables(kDefaultModuli, kMaxP);
+// The extraction's default-list kernel takes the 24-bit residue path for
+// every plane without a tie fix: each default modulus is 256 or odd, and >= 171.
+constexpr bool default_moduli_plain() {
+  for (int t = 0; t < kMaxP; ++t) {
+    const int p = kDefaultModuli[t];
+    if (p < 171 || (!(p & 1) && p != 256)) return false;
+  }
+  return true;
+}
+static_assert(default_moduli_plain(), "default moduli: 256 or odd, and >= 171");
 
 int gcd_int(int a, int b) {
   while (b) { const int t = a % b; a = b; b = t; }
@@ -156,8 +169,7 @@ ModTables make_tables(const int32_t* primes, int P) {
     T.p[t] = G.p[t];
     T.mib[t] = G.mib[t];
     T.invp[t] = G.invp[t];
-    const int c31 = (int)((1LL << 31) % primes[t]);
-    T.c31[t] = 2 * c31 > primes[t] ? c31 - primes[t] : c31;
+    T.c31[t] = G.c31[t];
     for (int g = 0; g < kGarnerWords; ++g) T.nmp[t * kGarnerWords + g] = G.nmp[t * kGarnerWords + g];
     l2 += (float)std::log2((double)primes[t]);
   }
@@ -533,8 +545,8 @@ struct ExtractArgs {
   int use_corr;
   int64_t nkt;       // Kp / 64
   int64_t planeA, planeB, memberA, memberB;
-  int64_t wgA;       // work groups of the A part; B follows
-  int64_t rgA, rgB;  // 64-row groups per member: Mp / 64, Np / 64
+  int64_t rgA, rgB;  // 64-row groups per member: Mp / 64, Np / 64 (0: B not extracted)
+  int64_t rgA_data, rgB_data;   // those holding operand rows: ceil(M / 64), ceil(N / 64)
   const int16_t* sftA;
   const int16_t* sftB;
   const int* bits_eff;
@@ -543,17 +555,36 @@ struct ExtractArgs {
   ModTables tab;
 };
 
+// kDefault: the modulus list is a prefix of the default one, whose constants
+// the plane loop takes at compile time (no scalar load and wait per plane,
+// which dominated small launches); otherwise the tables of the arguments.
+template <bool kDefault>
 __global__ void __launch_bounds__(kThreads)
 extract_kernel(ExtractArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // Work groups: the row groups holding operand rows of A, then of B, then
+  // the all-padding row groups of A and of B (zero stores only), so that the
+  // work spreads evenly over the XCDs (group i runs on XCD i % 8) whatever
+  // the padding.
   int64_t wg = blockIdx.x;
-  const bool isA = wg < a.wgA;
-  if (!isA) wg -= a.wgA;
+  const int64_t nA = a.batch * a.rgA_data * a.nkt, nB = a.batch * a.rgB_data * a.nkt;
+  const int64_t nAp = a.batch * (a.rgA - a.rgA_data) * a.nkt;
+  bool isA;
+  int64_t rg_per, rg_off = 0;
+  if (wg < nA) {
+    isA = true; rg_per = a.rgA_data;
+  } else if ((wg -= nA) < nB) {
+    isA = false; rg_per = a.rgB_data;
+  } else if ((wg -= nB) < nAp) {
+    isA = true; rg_per = a.rgA - a.rgA_data; rg_off = a.rgA_data;
+  } else {
+    wg -= nAp;
+    isA = false; rg_per = a.rgB - a.rgB_data; rg_off = a.rgB_data;
+  }
   const bool kn = !isA && a.b_kn;
   // Work group -> (member, 64-row group, k tile).  Row-major operands walk k
   // fastest (consecutive groups read consecutive bytes of the same rows);
   // the [K, N] operand walks the 64-column group fastest.
-  const int64_t rg_per = isA ? a.rgA : a.rgB;
   int64_t b, rg, kt;
   if (kn) {
     rg = wg % rg_per;
@@ -566,6 +597,7 @@ extract_kernel(ExtractArgs a) {
     rg = t % rg_per;
     b = t / rg_per;
   }
+  rg += rg_off;
   const int64_t R = isA ? a.M : a.N;
   const int64_t K = a.K;
   // Wave w covers rows 64 rg + 16 w .. +16 and the whole k tile: one
@@ -595,11 +627,6 @@ extract_kernel(ExtractArgs a) {
     return;
   }
 
-  // Shift: per row of A / of B [N,K]; per column of B [K,N] -- one per lane.
-  const int16_t* sfts = isA ? a.sftA : a.sftB;
-  const int be = a.bits_eff[0];
-  const int shift = rowok ? (int)sfts[b * R + r] + a.bits_eff[1] : 0;
-
   double x[16];
   if (!rowok || k0 >= K) {
 #pragma unroll
@@ -618,6 +645,12 @@ extract_kernel(ExtractArgs a) {
       for (int j = 0; j < 16; ++j) x[j] = (k0 + j < K) ? src[j] : 0.0;
     }
   }
+
+  // Shift: per row of A / of B [N,K]; per column of B [K,N] -- one per lane.
+  // Read after the operand loads are issued, so one round trip covers both.
+  const int16_t* sfts = isA ? a.sftA : a.sftB;
+  const int be = a.bits_eff[0];
+  const int shift = rowok ? (int)sfts[b * R + r] + a.bits_eff[1] : 0;
 
   // Split every element first: th, tl as exact doubles, hi7/q7 bytes.  All
   // scalings are by powers of two and exact: y = |x| 2^shift (< 2^be, or
@@ -664,8 +697,9 @@ extract_kernel(ExtractArgs a) {
   // a tie's +p/2 into barrett_bal32's -p/2.  Each variant is its own copy
   // of the loop, so the usual moduli carry no extra compare.
   auto plane_residues = [&](auto int_path, auto tie_fix, int pi) {
-    const int pt = a.tab.p[pi], c31 = a.tab.c31[pi];
-    const double ip = a.tab.invp[pi];
+    const int pt = kDefault ? kDefaultTab.p[pi] : a.tab.p[pi];
+    const int c31 = kDefault ? kDefaultTab.c31[pi] : a.tab.c31[pi];
+    const double ip = kDefault ? kDefaultTab.invp[pi] : a.tab.invp[pi];
     uint32_t w4[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -687,15 +721,22 @@ extract_kernel(ExtractArgs a) {
     *reinterpret_cast<v4i*>(base + pi * plane + off) =
         v4i{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
   };
-  for (int pi = 0; pi < P; ++pi) {
-    const int pt = a.tab.p[pi];
-    const bool tie = !(pt & 1) && pt != 256;
-    if (pt >= 171) {
-      if (!tie) plane_residues(std::true_type{}, std::false_type{}, pi);
-      else plane_residues(std::true_type{}, std::true_type{}, pi);
-    } else {
-      if (!tie) plane_residues(std::false_type{}, std::false_type{}, pi);
-      else plane_residues(std::false_type{}, std::true_type{}, pi);
+  if constexpr (kDefault) {
+    // Every default modulus is 256 or odd, and >= 171.
+#pragma unroll
+    for (int pi = 0; pi < kMaxP; ++pi)
+      if (pi < P) plane_residues(std::true_type{}, std::false_type{}, pi);
+  } else {
+    for (int pi = 0; pi < P; ++pi) {
+      const int pt = a.tab.p[pi];
+      const bool tie = !(pt & 1) && pt != 256;
+      if (pt >= 171) {
+        if (!tie) plane_residues(std::true_type{}, std::false_type{}, pi);
+        else plane_residues(std::true_type{}, std::true_type{}, pi);
+      } else {
+        if (!tie) plane_residues(std::false_type{}, std::false_type{}, pi);
+        else plane_residues(std::false_type{}, std::true_type{}, pi);
+      }
     }
   }
   if (a.use_corr) {
@@ -1240,6 +1281,14 @@ reconstruct_kernel(ReconArgs a) {
   const int P = kP > 0 ? kP : a.tab.P;
   constexpr bool kUsual = kP > 0;
   const int64_t boff = (mb * a.NB + nb) * 1024 + 4 * thr;  // byte (int8) / element (int32)
+  // The output scalings, read with the residues (one round trip, instead of
+  // a dependent load per element at the end); rows past M read row M - 1.
+  // Both shifts grew by bits_eff[1] at the width pick.
+  const int cshift = a.bits_eff[0] - 15;
+  const int sj = (int)a.sftB[b * a.N + j] + 2 * a.bits_eff[1];
+  int sai[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) sai[e] = (int)a.sftA[b * a.M + min(i0 + e, a.M - 1)];
   uint32_t w[kMaxP];
   int64_t cv[4] = {0, 0, 0, 0};
   if (kDeep) {
@@ -1396,10 +1445,6 @@ reconstruct_kernel(ReconArgs a) {
     }
   }
 
-  const int cshift = a.bits_eff[0] - 15;
-  // Both shifts grew by bits_eff[1] at the width pick.
-  const int sj = (int)a.sftB[b * a.N + j] + 2 * a.bits_eff[1];
-  const int16_t* sA = a.sftA + b * a.M + i0;
   double* outp = a.out + (b * a.M + i0) * a.N + j;
 
   // Horner per group of 7 (digits 7g .. 7g+6, high to low): group position
@@ -1431,7 +1476,7 @@ reconstruct_kernel(ReconArgs a) {
     // Every group ends on its position-0 digit, an int64 step, so ag holds
     // the group value whatever the group's digit count.
     const long long a0 = ag[e][0], a1 = ag[e][1], a2 = ag[e][2];
-    const int sh = -((int)sA[e] + sj);
+    const int sh = -(sai[e] + sj);
     double val;
     if (kExact) {
       i128 acc = ng == 3 ? (i128)a2 : (ng == 2 ? (i128)a1 : (i128)a0);
@@ -1668,6 +1713,8 @@ int run(const Call& c) {
       if (gsz > limit) return fail(FP64EMU_EINVAL, "problem too large for one launch");
   }
   const ModTables tab = make_tables(c.primes, c.P);
+  bool default_moduli = true;
+  for (int t = 0; t < c.P; ++t) default_moduli = default_moduli && c.primes[t] == kDefaultModuli[t];
 
   char* ws = static_cast<char*>(c.ws);
   int16_t* sftA = reinterpret_cast<int16_t*>(ws + L.off_sftA);
@@ -1740,12 +1787,15 @@ int run(const Call& c) {
       ea.planeA = L.planeA_bytes; ea.planeB = L.planeB_bytes;
       ea.memberA = L.memberA_bytes; ea.memberB = L.memberB_bytes;
       ea.rgA = L.chunk_rows / 64; ea.rgB = with_B ? L.Np / 64 : 0;
-      ea.wgA = c.batch * ea.rgA * nkt;
+      ea.rgA_data = (Mc + 63) / 64; ea.rgB_data = with_B ? (c.N + 63) / 64 : 0;
       ea.sftA = sftA + m0; ea.sftB = sftB; ea.bits_eff = bits_eff;
       ea.planesA = planesA; ea.planesB = planesB;
       ea.tab = tab;
-      const int64_t wg = ea.wgA + c.batch * ea.rgB * nkt;
-      hipLaunchKernelGGL(extract_kernel, dim3((unsigned)wg), dim3(kThreads), 0, s, ea);
+      const int64_t wg = c.batch * (ea.rgA + ea.rgB) * nkt;
+      if (default_moduli)
+        hipLaunchKernelGGL(extract_kernel<true>, dim3((unsigned)wg), dim3(kThreads), 0, s, ea);
+      else
+        hipLaunchKernelGGL(extract_kernel<false>, dim3((unsigned)wg), dim3(kThreads), 0, s, ea);
       if (c.ev) {
         if (int st = check_hip(hipEventRecord(c.ev[1], s), "hipEventRecord")) return st;
       }
