@@ -319,31 +319,64 @@ __device__ __forceinline__ void row_pass(const double* __restrict__ x, int64_t c
   }
 }
 
-__global__ void __launch_bounds__(kThreads)
-size_rows_kernel(const double* __restrict__ A, int64_t rowsA, const double* __restrict__ B,
-                 int64_t rows, int64_t K, int bits, int16_t* __restrict__ sftA,
-                 float* __restrict__ lgA, int16_t* __restrict__ sftB, float* __restrict__ lgB) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+// kGroup: few rows (not enough waves to fill the chip): a 256-thread group
+// per row, wave w running sum 64 w + l alone (sixteen of its loads in
+// flight), the four waves' sums meeting in LDS before the same fold.
+template <bool kGroup>
+__device__ __forceinline__ void size_rows_body(int64_t bid, const double* __restrict__ A, int64_t rowsA,
+                                               const double* __restrict__ B, int64_t rows, int64_t K,
+                                               int bits, int16_t* __restrict__ sftA,
+                                               float* __restrict__ lgA, int16_t* __restrict__ sftB,
+                                               float* __restrict__ lgB) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row = kGroup ? bid : bid * kRowsPerBlock + wave;
   if (row >= rows) return;
   const bool isA = row < rowsA;
   const int64_t r = isA ? row : row - rowsA;
   const double* __restrict__ x = (isA ? A : B) + r * K + lane;
   double mx = 0.0, ss[4] = {0.0, 0.0, 0.0, 0.0};
-  // Sixteen loads in flight, then eight, then guarded 256-element blocks.
-  int64_t c = 0;
-  for (; c + 1024 <= K; c += 1024) row_pass<4>(x, c, mx, ss);
-  if (c + 512 <= K) {
-    row_pass<2>(x, c, mx, ss);
-    c += 512;
-  }
-  for (; c < K; c += 256) {
+  if constexpr (kGroup) {
+    const double* __restrict__ xw = x + 64 * wave;
+    double sw = 0.0, mw = 0.0;
+    // Elements past K read as 0, which leaves both the max and the sum
+    // (never -0) unchanged.
+    for (int64_t c = 0; c < K; c += 4096) {
+      double v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        v[i] = c + 256 * i + 64 * wave + lane < K ? xw[c + 256 * i] : 0.0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        mw = fmax(mw, fabs(v[i]));
+        sw = fma(v[i], v[i], sw);
+      }
+    }
+    __shared__ double sh_ss[4][64], sh_mx[4][64];
+    sh_ss[wave][lane] = sw;
+    sh_mx[wave][lane] = mw;
+    __syncthreads();
+    if (wave != 0) return;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      if (c + 64 * u + lane < K) {
-        const double v = x[c + 64 * u];
-        mx = fmax(mx, fabs(v));
-        ss[u] = fma(v, v, ss[u]);
+      ss[u] = sh_ss[u][lane];
+      mx = fmax(mx, sh_mx[u][lane]);
+    }
+  } else {
+    // Sixteen loads in flight, then eight, then guarded 256-element blocks.
+    int64_t c = 0;
+    for (; c + 1024 <= K; c += 1024) row_pass<4>(x, c, mx, ss);
+    if (c + 512 <= K) {
+      row_pass<2>(x, c, mx, ss);
+      c += 512;
+    }
+    for (; c < K; c += 256) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (c + 64 * u + lane < K) {
+          const double v = x[c + 64 * u];
+          mx = fmax(mx, fabs(v));
+          ss[u] = fma(v, v, ss[u]);
+        }
       }
     }
   }
@@ -359,17 +392,40 @@ size_rows_kernel(const double* __restrict__ A, int64_t rowsA, const double* __re
   }
 }
 
+template <bool kGroup>
+__global__ void __launch_bounds__(kThreads)
+size_rows_kernel(const double* __restrict__ A, int64_t rowsA, const double* __restrict__ B,
+                 int64_t rows, int64_t K, int bits, int16_t* __restrict__ sftA,
+                 float* __restrict__ lgA, int16_t* __restrict__ sftB, float* __restrict__ lgB) {
+  size_rows_body<kGroup>(blockIdx.x, A, rowsA, B, rows, K, bits, sftA, lgA, sftB, lgB);
+}
+
+// A wave per row when the rows give the chip at least four waves per SIMD,
+// else a 256-thread group per row.
+constexpr int64_t kRowsGroupBelow = 4096;
+
+void launch_size_rows(int64_t rows, hipStream_t s, const double* A, int64_t rowsA, const double* B,
+                      int64_t K, int bits, int16_t* sftA, float* lgA, int16_t* sftB, float* lgB) {
+  if (rows < kRowsGroupBelow)
+    hipLaunchKernelGGL(size_rows_kernel<true>, dim3((unsigned)rows), dim3(kThreads), 0, s, A, rowsA,
+                       B, rows, K, bits, sftA, lgA, sftB, lgB);
+  else
+    hipLaunchKernelGGL(size_rows_kernel<false>, dim3((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock)),
+                       dim3(kThreads), 0, s, A, rowsA, B, rows, K, bits, sftA, lgA, sftB, lgB);
+}
+
 // Column partials of a [K, N] operand (per batch member): thread j owns
 // global column j, blockIdx.y a k-slab summed in order.
 // fp64_emu_cuda/fp64_emu.cu:148-169.
-__global__ void __launch_bounds__(kThreads)
-size_cols_partial_kernel(const double* __restrict__ X, int64_t totalcols, int64_t rows_per,
-                         int64_t cols_per, int64_t kslab, double* __restrict__ pmax,
-                         double* __restrict__ pss) {
-  const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+__device__ __forceinline__ void size_cols_partial_body(int64_t bx, int64_t by, const double* __restrict__ X,
+                                                       int64_t totalcols, int64_t rows_per,
+                                                       int64_t cols_per, int64_t kslab,
+                                                       double* __restrict__ pmax,
+                                                       double* __restrict__ pss) {
+  const int64_t j = bx * kThreads + threadIdx.x;
   if (j >= totalcols) return;
   const int64_t b = j / cols_per, n = j - b * cols_per;
-  const int64_t k0 = (int64_t)blockIdx.y * kslab;
+  const int64_t k0 = by * kslab;
   const int64_t k1 = min(k0 + kslab, rows_per);
   const double* __restrict__ base = X + b * rows_per * cols_per + n;
   double mx = 0.0, ss = 0.0;
@@ -390,38 +446,82 @@ size_cols_partial_kernel(const double* __restrict__ X, int64_t totalcols, int64_
     mx = fmax(mx, fabs(v));
     ss = fma(v, v, ss);
   }
-  pmax[(int64_t)blockIdx.y * totalcols + j] = mx;
-  pss[(int64_t)blockIdx.y * totalcols + j] = ss;
+  pmax[by * totalcols + j] = mx;
+  pss[by * totalcols + j] = ss;
 }
 
-// Slabs folded in order.  fp64_emu_cuda/fp64_emu.cu:171-189.
+// The sizing of A's rows and of the [K, N] operand's column slabs in one
+// launch: groups [0, nrow) size rows, the rest column slabs (x fastest).
+template <bool kGroup>
+__global__ void __launch_bounds__(kThreads)
+size_rows_cols_kernel(const double* __restrict__ A, int64_t rowsA, int64_t nrow, int64_t K, int bits,
+                      int16_t* __restrict__ sftA, float* __restrict__ lgA,
+                      const double* __restrict__ X, int64_t totalcols, int64_t cols_per,
+                      int64_t kslab, int64_t gcx, double* __restrict__ pmax,
+                      double* __restrict__ pss) {
+  const int64_t bid = blockIdx.x;
+  if (bid < nrow) {
+    size_rows_body<kGroup>(bid, A, rowsA, A, rowsA, K, bits, sftA, lgA, nullptr, nullptr);
+  } else {
+    const int64_t q = bid - nrow;
+    size_cols_partial_body(q % gcx, q / gcx, X, totalcols, K, cols_per, kslab, pmax, pss);
+  }
+}
+
+// Slabs folded in order.  fp64_emu_cuda/fp64_emu.cu:171-189.  A group
+// covers 64 columns: its 256 threads bring the columns' slab partials into
+// LDS (up to 64 loads in flight each, one round trip), then one lane per
+// column folds them in slab order.
+constexpr int kFinalCols = 64;
+
 __global__ void __launch_bounds__(kThreads)
 size_cols_final_kernel(const double* __restrict__ pmax, const double* __restrict__ pss,
                        int64_t totalcols, int nslab, int bits, int16_t* __restrict__ sft,
                        float* __restrict__ lg) {
-  const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (j >= totalcols) return;
-  double mx = 0.0, ss = 0.0;
-  // 32 slabs' loads in flight (few columns come with many slabs, up to 128:
-  // the fold is load-latency bound); the sum keeps the slab order.
-  constexpr int kInFlight = 32;
-  int s = 0;
-  for (; s + kInFlight <= nslab; s += kInFlight) {
-    double vm[kInFlight], vs[kInFlight];
+  __shared__ double sh_m[kMaxSlab * kFinalCols], sh_s[kMaxSlab * kFinalCols];
+  const int tid = threadIdx.x;
+  const int64_t j0 = (int64_t)blockIdx.x * kFinalCols;
+  const int n = nslab * kFinalCols;                      // entries f = slab * 64 + column
+  constexpr int kPer = kMaxSlab * kFinalCols / kThreads;  // 32
+  double vm[kPer], vs[kPer];
 #pragma unroll
-    for (int u = 0; u < kInFlight; ++u) {
-      vm[u] = pmax[(int64_t)(s + u) * totalcols + j];
-      vs[u] = pss[(int64_t)(s + u) * totalcols + j];
-    }
+  for (int i = 0; i < kPer; ++i) {
+    const int f = tid + kThreads * i;
+    const int64_t j = j0 + (f & (kFinalCols - 1));
+    const bool ok = f < n && j < totalcols;
+    const int64_t at = (int64_t)(f / kFinalCols) * totalcols + j;
+    vm[i] = ok ? pmax[at] : 0.0;
+    vs[i] = ok ? pss[at] : 0.0;
+  }
 #pragma unroll
-    for (int u = 0; u < kInFlight; ++u) {
-      mx = fmax(mx, vm[u]);
-      ss = ss + vs[u];
+  for (int i = 0; i < kPer; ++i) {
+    const int f = tid + kThreads * i;
+    if (f < n) {
+      sh_m[f] = vm[i];
+      sh_s[f] = vs[i];
     }
   }
-  for (; s < nslab; ++s) {
-    mx = fmax(mx, pmax[(int64_t)s * totalcols + j]);
-    ss = ss + pss[(int64_t)s * totalcols + j];
+  __syncthreads();
+  const int64_t j = j0 + tid;
+  if (tid >= kFinalCols || j >= totalcols) return;
+  double mx = 0.0, ss = 0.0;
+  int sl = 0;
+  for (; sl + 16 <= nslab; sl += 16) {   // sixteen LDS reads ahead of the adds
+    double m[16], v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      m[u] = sh_m[(sl + u) * kFinalCols + tid];
+      v[u] = sh_s[(sl + u) * kFinalCols + tid];
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      mx = fmax(mx, m[u]);
+      ss = ss + v[u];
+    }
+  }
+  for (; sl < nslab; ++sl) {
+    mx = fmax(mx, sh_m[sl * kFinalCols + tid]);
+    ss = ss + sh_s[sl * kFinalCols + tid];
   }
   row_stats_out(mx, ss, bits, &sft[j], &lg[j]);
 }
@@ -1731,19 +1831,23 @@ int run(const Call& c) {
 
   // 1. sizing
   if (!c.b_kn) {
-    hipLaunchKernelGGL(size_rows_kernel, dim3((unsigned)((MF + NF + kRowsPerBlock - 1) / kRowsPerBlock)),
-                       dim3(kThreads), 0, s, c.A, MF, c.B, MF + NF, c.K, c.bits, sftA, lgA, sftB, lgB);
+    launch_size_rows(MF + NF, s, c.A, MF, c.B, c.K, c.bits, sftA, lgA, sftB, lgB);
   } else {
-    hipLaunchKernelGGL(size_rows_kernel, dim3((unsigned)((MF + kRowsPerBlock - 1) / kRowsPerBlock)),
-                       dim3(kThreads), 0, s, c.A, MF, c.A, MF, c.K, c.bits, sftA, lgA, sftB, lgB);
     int64_t kslab; int nslab;
     slab_split(NF, c.K, &kslab, &nslab);
-    const unsigned gcx = (unsigned)((NF + kThreads - 1) / kThreads);
-    if (nslab > 0)
-      hipLaunchKernelGGL(size_cols_partial_kernel, dim3(gcx, (unsigned)nslab), dim3(kThreads), 0, s,
-                         c.B, NF, c.K, c.N, kslab, pmax, pss);
-    hipLaunchKernelGGL(size_cols_final_kernel, dim3(gcx), dim3(kThreads), 0, s, pmax, pss, NF,
-                       nslab, c.bits, sftB, lgB);
+    const int64_t gcx = (NF + kThreads - 1) / kThreads;
+    // K > 0 here, so nslab >= 1.
+    const bool group = MF < kRowsGroupBelow;
+    const int64_t nrow = group ? MF : (MF + kRowsPerBlock - 1) / kRowsPerBlock;
+    const unsigned grid = (unsigned)(nrow + gcx * nslab);
+    if (group)
+      hipLaunchKernelGGL(size_rows_cols_kernel<true>, dim3(grid), dim3(kThreads), 0, s, c.A, MF, nrow,
+                         c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, gcx, pmax, pss);
+    else
+      hipLaunchKernelGGL(size_rows_cols_kernel<false>, dim3(grid), dim3(kThreads), 0, s, c.A, MF, nrow,
+                         c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, gcx, pmax, pss);
+    hipLaunchKernelGGL(size_cols_final_kernel, dim3((unsigned)((NF + kFinalCols - 1) / kFinalCols)),
+                       dim3(kThreads), 0, s, pmax, pss, NF, nslab, c.bits, sftB, lgB);
   }
   hipLaunchKernelGGL(pick_width_kernel, dim3(1), dim3(kPickThreads), 0, s, lgA, MF, lgB, NF,
                      std::min(tab.log2M, 126.0f), c.bits, bits_eff);
