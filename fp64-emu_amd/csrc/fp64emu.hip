@@ -215,15 +215,23 @@ int choose_ksplit(int64_t batch, int64_t tiles, int64_t nkt, int P, int ncorr) {
   return best;
 }
 
-// The narrow GEMM (256 x 128 tiles, two groups per CU) for products whose
-// groups are short (k-steps <= kNarrowMaxSteps; the fused correction slot
-// runs twice as many) and numerous enough to give every CU two.
+// The narrow GEMM (256 x 128 tiles, two groups per CU):
+// - for products whose groups are short (k-steps <= kNarrowMaxSteps; the
+//   fused correction slot runs twice as many) and numerous enough to give
+//   every CU two, so that groups overlap their prologues and epilogues;
+// - for products whose 256-column tiles are mostly padding: 128-column tiles
+//   cover N with at most 127 padded columns, worth it where that cuts the
+//   MFMA work by more than the narrow loop's ~10% lower efficiency at depth
+//   (e.g. N = 128: half the work).
 constexpr int64_t kNarrowMaxSteps = 16;
 
 bool use_narrow_gemm(const fp64emu_layout_t& L) {
-  if (L.deep || L.ksplit != 1 || L.Kp / kTileK > kNarrowMaxSteps) return false;
+  if (L.deep) return false;
+  const int64_t cols128 = (L.N + 127) / 128 * 128;
+  if (cols128 * 11 < L.Np * 10) return true;
+  if (L.ksplit != 1 || L.Kp / kTileK > kNarrowMaxSteps) return false;
   const int64_t groups = (int64_t)(L.nprimes + L.ncorr) * L.batch * (L.chunk_rows / kTileR) *
-                         ((L.N + 127) / 128);
+                         (cols128 / 128);
   return groups >= 2 * kCUs;
 }
 
