@@ -1555,15 +1555,17 @@ reconstruct_kernel(ReconArgs a) {
 
   double* outp = a.out + (b * a.M + i0) * a.N + j;
 
-  // Horner per group of 7 (digits 7g .. 7g+6, high to low): group position
-  // 6..3 in int32 (four balanced digits stay below 2^31; three below 2^23,
-  // so the 24-bit multiply is exact), positions 2..0 in int64.
-  int h32[4][3];
-  long long ag[4][3];
+  // Horner per group of 7 (digits 7g .. 7g+6, high to low), in two int32
+  // halves: positions 6..3 give H (four balanced digits stay below 2^31;
+  // three below 2^23, so the 24-bit multiplies are exact), positions 2..0
+  // give L (|L| < 2^23); the group value is H (p_0 p_1 p_2) + L, one 32 x 32
+  // -> 64-bit multiply-add (p_i the group's first three moduli; a group of at
+  // most three digits has H = 0).
+  int h32[4][3], l32[4][3];
 #pragma unroll
   for (int e = 0; e < 4; ++e)
 #pragma unroll
-    for (int g = 0; g < 3; ++g) { h32[e][g] = 0; ag[e][g] = 0; }
+    for (int g = 0; g < 3; ++g) { h32[e][g] = 0; l32[e][g] = 0; }
 #pragma unroll
   for (int t = kMaxP - 1; t >= 0; --t) {
     if (t >= P) continue;
@@ -1571,9 +1573,17 @@ reconstruct_kernel(ReconArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       if (pos >= 3) h32[e][g] = __mul24(h32[e][g], tab_p(t)) + dg[e][t];
-      else if (pos == 2) ag[e][g] = (long long)h32[e][g] * tab_p(t) + dg[e][t];
-      else ag[e][g] = ag[e][g] * tab_p(t) + dg[e][t];
+      else l32[e][g] = __mul24(l32[e][g], tab_p(t)) + dg[e][t];
     }
+  }
+  long long ag[4][3];
+#pragma unroll
+  for (int g = 0; g < 3; ++g) {
+    const int t0 = 7 * g;
+    // p_0 p_1 p_2 of group g (< 2^24); moduli past P only meet H = 0.
+    const int p3 = t0 + 2 < kMaxP ? tab_p(t0) * tab_p(t0 + 1) * tab_p(t0 + 2) : 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ag[e][g] = (long long)h32[e][g] * p3 + l32[e][g];
   }
 
   const int ng = (P + 6) / 7;
