@@ -267,14 +267,22 @@ def run_configs(steps, warmup):
         nat = (lambda: torch.bmm(A, B)) if batched else (lambda: A @ B)
 
         def timed(fn):
+            # At least `steps` calls and about 50 ms of them (small configs
+            # take tens of microseconds, where a handful of calls would time
+            # mostly the host's synchronisation).
             for _ in range(warmup):
                 fn()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            for _ in range(steps):
+            fn()
+            torch.cuda.synchronize()
+            one = time.perf_counter() - t0
+            n = max(steps, min(500, int(0.05 / max(one, 1e-6))))
+            t0 = time.perf_counter()
+            for _ in range(n):
                 fn()
             torch.cuda.synchronize()
-            return (time.perf_counter() - t0) * 1e3 / steps
+            return (time.perf_counter() - t0) * 1e3 / n
 
         ms = timed(emu)
         nat_ms = timed(nat)
