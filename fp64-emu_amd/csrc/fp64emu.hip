@@ -976,35 +976,47 @@ struct GemmShape {
   static constexpr int kCols = 32 * kWN;                 // tile columns
 };
 
-template <bool kDeep, int kWN>
-__global__ void __launch_bounds__(kThreads, kWN == 8 ? 1 : 2)
-modgemm_kernel(GemmArgs g) {
-  using Sh = GemmShape<kWN>;
-  constexpr int kS = Sh::kS, kSB = Sh::kSB, kDma = Sh::kDma, kHB = Sh::kHB;
-  __shared__ __attribute__((aligned(1024))) int8_t lds[kS * kSB];
+// Work item of a group: XCD-aware order -- work group i runs on XCD i % 8;
+// within each full chunk of 256 groups, XCD x takes logical items
+// 32x .. 32x+31, an 8x4 block of tiles sharing 12 operand panels in that
+// XCD's L2, while all XCDs work on the same slot (whose planes then stay
+// resident in the MALL).
+struct GemmItem {
+  int split, slot, mt, nt;
+  int64_t b;
+};
 
-  // XCD-aware order: work group i runs on XCD i % 8.  Within each full chunk
-  // of 256 groups, XCD x takes logical items 32x .. 32x+31, an 8x4 block of
-  // tiles sharing 12 operand panels in that XCD's L2, while all XCDs work on
-  // the same slot (whose planes then stay resident in the MALL).
+__device__ __forceinline__ GemmItem gemm_item(const GemmArgs& g) {
   const int64_t i = blockIdx.x;
   int64_t L = i;
   if ((i >> 8) < (g.total >> 8)) L = (i & ~255ll) + (i & 7) * 32 + ((i & 255) >> 3);
   const int64_t tiles = (int64_t)g.TM * g.TN;
   const int64_t sbs = L / tiles;                       // (slot, member, split)
   const int tile = (int)(L - sbs * tiles);
-  const int split = (int)(sbs % g.ksplit);
+  GemmItem it;
+  it.split = (int)(sbs % g.ksplit);
   const int64_t sb = sbs / g.ksplit;
-  const int slot = (int)(sb / g.batch);
-  const int64_t b = sb - (int64_t)slot * g.batch;
+  it.slot = (int)(sb / g.batch);
+  it.b = sb - (int64_t)it.slot * g.batch;
   // Grouped tile order: 8 row tiles per group, column-major inside.
   const int GM = 8;
   const int grp = tile / (GM * g.TN);
   const int first_m = grp * GM;
   const int gm = min(g.TM - first_m, GM);
   const int within = tile - grp * GM * g.TN;
-  const int mt = first_m + within % gm;
-  const int nt = within / gm;
+  it.mt = first_m + within % gm;
+  it.nt = within / gm;
+  return it;
+}
+
+// One output tile of one slot: the body of the GEMM kernels, on the group's
+// LDS ring `lds` (the kernel's single LDS object).
+template <bool kDeep, int kWN>
+__device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, const GemmItem it) {
+  using Sh = GemmShape<kWN>;
+  constexpr int kS = Sh::kS, kSB = Sh::kSB, kDma = Sh::kDma, kHB = Sh::kHB;
+  const int split = it.split, slot = it.slot, mt = it.mt, nt = it.nt;
+  const int64_t b = it.b;
 
   // Slot -> operand plane, k-tile window and output.
   const bool is_corr = slot < g.ncorr;
@@ -1302,6 +1314,28 @@ modgemm_kernel(GemmArgs g) {
         }
         __builtin_amdgcn_sched_barrier(0);
       }
+  }
+}
+
+template <bool kDeep, int kWN>
+__global__ void __launch_bounds__(kThreads, kWN == 8 ? 1 : 2)
+modgemm_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) int8_t lds[GemmShape<kWN>::kS * GemmShape<kWN>::kSB];
+  modgemm_tile<kDeep, kWN>(g, lds, gemm_item(g));
+}
+
+// 256-column tiles, except that the last tile column holds at most 128
+// columns of N: its groups run the narrow body on the tile's first half
+// (half the MFMA work of a 256-column tile of mostly padding).
+__global__ void __launch_bounds__(kThreads, 1)
+modgemm_mixed_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) int8_t lds[GemmShape<8>::kS * GemmShape<8>::kSB];
+  GemmItem it = gemm_item(g);
+  if (it.nt == g.TN - 1) {
+    it.nt *= 2;
+    modgemm_tile<false, 4>(g, lds, it);
+  } else {
+    modgemm_tile<false, 8>(g, lds, it);
   }
 }
 
@@ -1884,6 +1918,10 @@ int run(const Call& c) {
   // Shallow products with many groups run the narrow kernel (two groups per
   // CU); its column tiles past N hold only padding and are not launched.
   const bool narrow = L.gemm_tile_cols == 128;
+  // Wide tiles whose last tile column holds at most 128 columns of N: that
+  // column runs 128-column tiles in the same launch.
+  const bool mixed = !narrow && !L.deep && L.Np / kTileR >= 2 && c.N % kTileR != 0 &&
+                     c.N % kTileR <= 128;
   ga.TM = (int)(L.chunk_rows / kTileR);
   ga.TN = narrow ? (int)((c.N + 127) / 128) : (int)(L.Np / kTileR);
   ga.NB = L.Np / 64;
@@ -1927,6 +1965,8 @@ int run(const Call& c) {
         hipLaunchKernelGGL((modgemm_kernel<true, 8>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       else if (narrow)
         hipLaunchKernelGGL((modgemm_kernel<false, 4>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+      else if (mixed)
+        hipLaunchKernelGGL(modgemm_mixed_kernel, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       else
         hipLaunchKernelGGL((modgemm_kernel<false, 8>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       for (int t = 0; t < c.P && !L.deep; ++t) {

@@ -266,3 +266,25 @@ def test_narrow_tile_parity(dev, kind, batch, M, N, K, primes, corr):
         A = _randn((M, K), seed, dev)
         B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
     check_call(kind, A, B, primes, use_corr=corr)
+
+
+@pytest.mark.parametrize("kind,batch,M,N,K", [
+    ("mm", 1, 300, 1290, 200),        # last tile column: 10 of 256 columns
+    ("mm_nt", 1, 64, 1300, 20000),    # the same under a K-split
+    ("bmm", 2, 100, 1408, 130),       # 128 of 256: the narrow half exactly full
+])
+def test_mixed_tile_parity(dev, kind, batch, M, N, K):
+    """Wide GEMM tiles whose last tile column holds at most 128 columns of N
+    run that column as 128-column tiles in the same launch."""
+    from fp64_emu import capi
+    print(f"case mixed tiles {kind} b={batch} {M}x{N}x{K}", flush=True)
+    L = capi.layout(batch, M, N, K, 14, True)
+    assert L.gemm_tile_cols == 256 and 0 < N % 256 <= 128 and L.Np // 256 >= 2
+    seed = 900 + M + N + K
+    if kind == "bmm":
+        A = _randn((batch, M, K), seed, dev)
+        B = _randn((batch, N, K), seed + 1, dev)
+    else:
+        A = _randn((M, K), seed, dev)
+        B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
+    check_call(kind, A, B, O.PRIMES[:14])
