@@ -139,28 +139,34 @@ def test_mm_nt_and_mm_layouts_agree(dev):
     assert torch.equal(emu.mm_nt(A, Bt), emu.mm(A, Bt.t().contiguous()))
 
 
-def test_graph_capture_replays(dev):
+@pytest.mark.parametrize("kind,M,N,K", [
+    ("mm", 128, 96, 256),          # row sizing, narrow GEMM tiles
+    ("mm_nt", 64, 1300, 20000),    # fused row/column sizing, mixed tiles, K-split
+])
+def test_graph_capture_replays(dev, kind, M, N, K):
     """test_fp64_emu.py:164-182, strengthened: several replays with eager work
     and synchronisation between them; each replay equals the eager result on
     the buffers' current contents."""
-    print("case graph_capture_replays", flush=True)
-    A = _randn((128, 256), 15, dev)
-    B = _randn((96, 256), 16, dev)
+    print(f"case graph_capture_replays {kind} {M}x{N}x{K}", flush=True)
+    shapeB = (N, K) if kind == "mm" else (K, N)
+    fn = emu.mm if kind == "mm" else emu.mm_nt
+    A = _randn((M, K), 15, dev)
+    B = _randn(shapeB, 16, dev)
     for _ in range(3):
-        emu.mm(A, B)
+        fn(A, B)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        C = emu.mm(A, B)
+        C = fn(A, B)
     for r in range(4):
-        A.copy_(_randn((128, 256), 100 + r, dev))
-        B.copy_(_randn((96, 256), 200 + r, dev))
+        A.copy_(_randn((M, K), 100 + r, dev))
+        B.copy_(_randn(shapeB, 200 + r, dev))
         g.replay()
         torch.cuda.synchronize()
-        eager = emu.mm(A, B)
+        eager = fn(A, B)
         torch.cuda.synchronize()
         assert torch.equal(C, eager), f"replay {r}"
-        emu.mm_nt(A, B.t().contiguous())   # unrelated eager work between replays
+        emu.mm_nt(A, _randn((K, 40), 300 + r, dev))   # unrelated eager work between replays
 
 
 def test_torch_compile_traces(dev):
