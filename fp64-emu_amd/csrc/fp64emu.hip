@@ -289,6 +289,11 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
                      (size_t)(L->ksplit * batch * L->ncorr * L->outplane_bytes));
   L->total = o;
   L->gemm_tile_cols = use_narrow_gemm(*L) ? 128 : 256;
+  // 128 x 128 tiles where 128-row tiles also cut the padded work by > 10%
+  // (M <= 128: half): two groups per CU, a quarter of the 256 x 256 work.
+  const int64_t rows128 = (std::max<int64_t>(M, 1) + 127) / 128 * 128;
+  L->gemm_tile_rows = (L->gemm_tile_cols == 128 && L->nchunk == 1 && rows128 * 11 < L->Mp * 10)
+                          ? 128 : 256;
 }
 
 // ---------------------------------------------------------------------------
@@ -959,21 +964,25 @@ __device__ __forceinline__ void mfma_fence() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Two tile shapes.  kWN = 8: 256 x 256 output tiles, each wave 128 x 128
-// (8 x 8 accumulator quads, half the register file: one group per CU), a
-// 4-stage ring of 32 KiB.  kWN = 4: 256 x 128 tiles, each wave 128 x 64, a
-// 3-stage ring of 24 KiB, two groups per CU: for shallow products, whose
-// groups run only a few k-steps, one group's prologue and epilogue (operand
-// latency, residue stores) overlap the other's MFMAs.  Both copy stage
-// kt + 3 during k-step kt.
-template <int kWN>
+// Three tile shapes (kWM x kWN fragments of 16 per wave, 2 x 2 waves):
+// (8, 8): 256 x 256 output tiles, each wave 128 x 128 (8 x 8 accumulator
+// quads, half the register file: one group per CU), a 4-stage ring of
+// 32 KiB.  (8, 4): 256 x 128 tiles, each wave 128 x 64, a 3-stage ring of
+// 24 KiB, two groups per CU: for shallow products, whose groups run only a
+// few k-steps, one group's prologue and epilogue (operand latency, residue
+// stores) overlap the other's MFMAs; and where 128 columns cover N with less
+// padding.  (4, 4): 128 x 128 tiles, each wave 64 x 64, a 4-stage ring of
+// 16 KiB, two groups per CU: products whose rows and columns both fit 128-wide
+// tiles with less padding.  All copy stage kt + 3 during k-step kt.
+template <int kWM, int kWN>
 struct GemmShape {
-  static constexpr int kS = kWN == 8 ? 4 : 3;            // LDS ring stages
-  static constexpr int kBBytes = kWN * 2048;             // B tile: 32 kWN columns x 64 k
-  static constexpr int kSB = kTileBytes + kBBytes;       // stage: A tile then B tile
-  static constexpr int kDma = 4 + kWN / 2;               // copies per wave per stage
-  static constexpr int kHB = kWN / 4;                    // 64-column output blocks per wave
-  static constexpr int kCols = 32 * kWN;                 // tile columns
+  static constexpr int kS = (kWM == 8 && kWN == 4) ? 3 : 4;      // LDS ring stages
+  static constexpr int kABytes = kWM * 2048;                      // A tile: 32 kWM rows x 64 k
+  static constexpr int kBBytes = kWN * 2048;                      // B tile: 32 kWN columns x 64 k
+  static constexpr int kSB = kABytes + kBBytes;                   // stage: A tile then B tile
+  static constexpr int kDma = kWM / 2 + kWN / 2;                  // copies per wave per stage
+  static constexpr int kHB = kWN / 4;                             // 64-column output blocks per wave
+  static constexpr int kGroupsPerCU = (kWM == 8 && kWN == 8) ? 1 : 2;
 };
 
 // Work item of a group: XCD-aware order -- work group i runs on XCD i % 8;
@@ -1011,10 +1020,11 @@ __device__ __forceinline__ GemmItem gemm_item(const GemmArgs& g) {
 
 // One output tile of one slot: the body of the GEMM kernels, on the group's
 // LDS ring `lds` (the kernel's single LDS object).
-template <bool kDeep, int kWN>
+template <bool kDeep, int kWM, int kWN>
 __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, const GemmItem it) {
-  using Sh = GemmShape<kWN>;
+  using Sh = GemmShape<kWM, kWN>;
   constexpr int kS = Sh::kS, kSB = Sh::kSB, kDma = Sh::kDma, kHB = Sh::kHB;
+  constexpr int kAB = Sh::kABytes;
   const int split = it.split, slot = it.slot, mt = it.mt, nt = it.nt;
   const int64_t b = it.b;
 
@@ -1029,9 +1039,12 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   const int nk = max(0, min(klen, ktot - kbeg));
   const int kt0 = ((is_corr && g.ncorr == 2) ? slot * g.nkt : 0) + kbeg;
 
+  // A 128-row (or 128-column) tile is one half (8 fragments) of a 256-row
+  // plane tile.
+  const int mrt = kWM == 8 ? mt : mt >> 1;
+  const int mhalf = kWM == 8 ? 0 : mt & 1;
   const int8_t* At = g.A + b * g.memberA + (int64_t)plane * g.planeA +
-                     ((int64_t)mt * rstride + kt0) * kTileBytes;
-  // A narrow column tile is one half (8 fragments) of a 256-row plane tile.
+                     ((int64_t)mrt * rstride + kt0) * kTileBytes + mhalf * kAB;
   const int nrt = kWN == 8 ? nt : nt >> 1;
   const int nhalf = kWN == 8 ? 0 : nt & 1;
   const int8_t* Bt = g.B + b * g.memberB + (int64_t)plane * g.planeB +
@@ -1041,27 +1054,29 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  // Each wave copies fragments 4*wave .. 4*wave+3 of the A tile and
-  // kWN/2 of the B tile (2 KiB or 1 KiB blocks): the instruction offset
-  // advances the global and the LDS address alike.
-  const uint32_t goff = (uint32_t)(wave * 4096 + lane * 16);
+  // Each wave copies kWM/2 fragments of the A tile and kWN/2 of the B tile
+  // (blocks of 4 or 2 KiB): the instruction offset advances the global and
+  // the LDS address alike.
+  const uint32_t goff = (uint32_t)(wave * (kWM / 2) * 1024 + lane * 16);
   const uint32_t goffB = (uint32_t)(wave * (kWN / 2) * 1024 + lane * 16);
 #define FP64EMU_SLOT(kt) ((kS == 4) ? ((kt) & 3) : ((kt) % kS))
 #define FP64EMU_COPY_A(kt, j)                                                               \
   __builtin_amdgcn_global_load_lds(At + (int64_t)(kt) * kTileBytes + goff,                  \
-                                   (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + wave * 4096),   \
+                                   (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + wave * (kWM / 2) * 1024), \
                                    16, (j) * 1024, 0)
 #define FP64EMU_COPY_B(kt, j)                                                               \
   __builtin_amdgcn_global_load_lds(Bt + (int64_t)(kt) * kTileBytes + goffB,                 \
-                                   (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + kTileBytes +    \
+                                   (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + kAB +           \
                                              wave * (kWN / 2) * 1024),                      \
                                    16, (j) * 1024, 0)
 #define FP64EMU_ISSUE(kt)                                                              \
   do {                                                                                 \
     FP64EMU_COPY_A(kt, 0);                                                             \
     FP64EMU_COPY_A(kt, 1);                                                             \
-    FP64EMU_COPY_A(kt, 2);                                                             \
-    FP64EMU_COPY_A(kt, 3);                                                             \
+    if constexpr (kWM == 8) {                                                          \
+      FP64EMU_COPY_A(kt, 2);                                                           \
+      FP64EMU_COPY_A(kt, 3);                                                           \
+    }                                                                                  \
     FP64EMU_COPY_B(kt, 0);                                                             \
     FP64EMU_COPY_B(kt, 1);                                                             \
     if constexpr (kWN == 8) {                                                          \
@@ -1069,19 +1084,20 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
       FP64EMU_COPY_B(kt, 3);                                                           \
     }                                                                                  \
   } while (0)
-  // Fragments of one k-step: F[0..7] = A row blocks 8 wm .. 8 wm + 7 (16 rows
-  // x 64 k each), F[8..8+kWN) = B column blocks kWN wn .. kWN wn + kWN - 1.
+  // Fragments of one k-step: F[0..kWM) = A row blocks kWM wm .. kWM wm +
+  // kWM - 1 (16 rows x 64 k each), F[kWM..kWM+kWN) = B column blocks kWN wn ..
+  // kWN wn + kWN - 1.
 #define FP64EMU_READF(F, kt)                                                               \
   do {                                                                                     \
     const v4i* sa_ = reinterpret_cast<const v4i*>(lds + FP64EMU_SLOT(kt) * kSB);          \
-    const v4i* sb_ = sa_ + kTileBytes / 16;                                                \
-    _Pragma("unroll") for (int y = 0; y < kWN; ++y) F[8 + y] = sb_[(wn * kWN + y) * 64 + lane]; \
-    _Pragma("unroll") for (int x = 0; x < 8; ++x) F[x] = sa_[(wm * 8 + x) * 64 + lane];     \
+    const v4i* sb_ = sa_ + kAB / 16;                                                       \
+    _Pragma("unroll") for (int y = 0; y < kWN; ++y) F[kWM + y] = sb_[(wn * kWN + y) * 64 + lane]; \
+    _Pragma("unroll") for (int x = 0; x < kWM; ++x) F[x] = sa_[(wm * kWM + x) * 64 + lane]; \
   } while (0)
 #define FP64EMU_MMA(F, MMA)                                                                 \
   do {                                                                                      \
-    _Pragma("unroll") for (int x = 0; x < 8; ++x)                                           \
-    _Pragma("unroll") for (int y = 0; y < kWN; ++y) MMA(acc[x][y], F[x], F[8 + y]);         \
+    _Pragma("unroll") for (int x = 0; x < kWM; ++x)                                         \
+    _Pragma("unroll") for (int y = 0; y < kWN; ++y) MMA(acc[x][y], F[x], F[kWM + y]);       \
   } while (0)
   // One k-step: stage kt+1 must have landed (own copies: at most one later
   // group in flight), then the barrier makes every wave's copies visible
@@ -1109,7 +1125,8 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   // and the six copies spread as A 0, 1 | A 2 | A 3, B 0 | B 1.)
 #define FP64EMU_CHUNK(kt, FC, FN, c, MMA)                                                    \
   do {                                                                                       \
-    if constexpr (kWN == 4) FP64EMU_CHUNK_N(kt, FC, FN, c, MMA);                             \
+    if constexpr (kWM == 4) FP64EMU_CHUNK_S(kt, FC, FN, c, MMA);                             \
+    else if constexpr (kWN == 4) FP64EMU_CHUNK_N(kt, FC, FN, c, MMA);                        \
     else FP64EMU_CHUNK_W(kt, FC, FN, c, MMA);                                                \
   } while (0)
 #define FP64EMU_CHUNK_W(kt, FC, FN, c, MMA)                                                  \
@@ -1157,6 +1174,25 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
       __builtin_amdgcn_sched_barrier(0);                                                     \
     }                                                                                        \
   } while (0)
+  // (4, 4): chunk c runs A block c against B 0..3 (four MFMAs) with two reads
+  // of the next step's fragments (B 0, 1 | B 2, 3 | A 0, 1 | A 2, 3) and one
+  // copy (A 0 | A 1 | B 0 | B 1).
+#define FP64EMU_CHUNK_S(kt, FC, FN, c, MMA)                                                  \
+  do {                                                                                       \
+    const v4i* sa_ = reinterpret_cast<const v4i*>(lds + FP64EMU_SLOT((kt) + 1) * kSB);      \
+    const v4i* sb_ = sa_ + kAB / 16;                                                         \
+    if constexpr ((c) <= 1) FP64EMU_COPY_A((kt) + 3, (c));                                   \
+    else FP64EMU_COPY_B((kt) + 3, (c) - 2);                                                  \
+    _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                          \
+      __builtin_amdgcn_sched_barrier(0);                                                     \
+      const int f_ = (c) * 2 + j;                                                            \
+      if (f_ < 4) FN[4 + f_] = sb_[(wn * 4 + f_) * 64 + lane];                               \
+      else FN[f_ - 4] = sa_[(wm * 4 + f_ - 4) * 64 + lane];                                  \
+      __builtin_amdgcn_sched_barrier(0);                                                     \
+      _Pragma("unroll") for (int u = 0; u < 2; ++u) MMA(acc[(c)][2 * j + u], FC[(c)], FC[4 + 2 * j + u]); \
+      __builtin_amdgcn_sched_barrier(0);                                                     \
+    }                                                                                        \
+  } while (0)
 #define FP64EMU_STEP_FULL(kt, FC, FN, MMA)                                                   \
   do {                                                                                       \
     wait_vm_lgkm0<kDma>();                                                                   \
@@ -1167,18 +1203,18 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     FP64EMU_CHUNK(kt, FC, FN, 3, MMA);                                                       \
   } while (0)
 
-  v4i acc[8][kWN];
+  v4i acc[kWM][kWN];
   if (nk == 0) {
     // A trailing K-split group past the end: its outputs are zeros.
 #pragma unroll
-    for (int x = 0; x < 8; ++x)
+    for (int x = 0; x < kWM; ++x)
 #pragma unroll
       for (int y = 0; y < kWN; ++y) acc[x][y] = v4i{0, 0, 0, 0};
   } else {
 #pragma unroll
     for (int s = 0; s < 3; ++s)
       if (s < nk) FP64EMU_ISSUE(s);
-    v4i F0[8 + kWN], F1[8 + kWN];
+    v4i F0[kWM + kWN], F1[kWM + kWN];
     wait_vm_lgkm0<0>();
     barrier_lds();
     FP64EMU_READF(F0, 0);
@@ -1211,23 +1247,24 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
 #undef FP64EMU_CHUNK
 #undef FP64EMU_CHUNK_W
 #undef FP64EMU_CHUNK_N
+#undef FP64EMU_CHUNK_S
 #undef FP64EMU_STEP_FULL
 #undef FP64EMU_COPY_A
 #undef FP64EMU_COPY_B
 #undef FP64EMU_SLOT
 
-  // Epilogue: output blocks of 16 rows x 64 columns; this wave's 128 x
-  // 16 kWN holds 8 row blocks x kWN/4 column blocks.  Element 16 l + 4 q + v
+  // Epilogue: output blocks of 16 rows x 64 columns; this wave's 16 kWM x
+  // 16 kWN holds kWM row blocks x kWN/4 column blocks.  Element 16 l + 4 q + v
   // of a block is lane l's value v of accumulator column block q (row
   // 4 (l / 16) + v, column 16 q + l % 16).
   const int64_t NB = g.NB;
-  const int64_t rb0 = (int64_t)mt * 16 + wm * 8, cb0 = (int64_t)nt * (kWN / 2) + wn * kHB;
+  const int64_t rb0 = (int64_t)mt * (2 * kWM) + wm * kWM, cb0 = (int64_t)nt * (kWN / 2) + wn * kHB;
   if (kDeep && is_corr) {
     // K-segmented: this segment's correction products join the int64 sum.
     typedef long long v2l __attribute__((ext_vector_type(2)));
     int64_t* dst = g.cacc + b * g.outplane;
 #pragma unroll
-    for (int x = 0; x < 8; ++x)
+    for (int x = 0; x < kWM; ++x)
 #pragma unroll
       for (int h = 0; h < kHB; ++h) {
         v2l* d = reinterpret_cast<v2l*>(dst + ((rb0 + x) * NB + cb0 + h) * 1024 + lane * 16);
@@ -1252,7 +1289,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     const int half_lo = -(g.p[t] >> 1);
     int32_t* dst = g.racc + (b * g.P + t) * g.outplane;
 #pragma unroll
-    for (int x = 0; x < 8; ++x)
+    for (int x = 0; x < kWM; ++x)
 #pragma unroll
       for (int h = 0; h < kHB; ++h) {
         v4i* d = reinterpret_cast<v4i*>(dst + ((rb0 + x) * NB + cb0 + h) * 1024 + lane * 16);
@@ -1285,7 +1322,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     int32_t* cdst = g.corr + (sbm * g.ncorr + (is_corr ? slot : 0)) * g.outplane;
     int8_t* rdst = g.res8 + (sbm * g.P + t) * g.outplane;
 #pragma unroll
-    for (int x = 0; x < 8; ++x)
+    for (int x = 0; x < kWM; ++x)
 #pragma unroll
       for (int h = 0; h < kHB; ++h) {
         const int64_t blk = ((rb0 + x) * NB + cb0 + h) * 1024 + lane * 16;
@@ -1317,11 +1354,12 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   }
 }
 
-template <bool kDeep, int kWN>
-__global__ void __launch_bounds__(kThreads, kWN == 8 ? 1 : 2)
+template <bool kDeep, int kWM, int kWN>
+__global__ void __launch_bounds__(kThreads, (kWM == 8 && kWN == 8) ? 1 : 2)
 modgemm_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) int8_t lds[GemmShape<kWN>::kS * GemmShape<kWN>::kSB];
-  modgemm_tile<kDeep, kWN>(g, lds, gemm_item(g));
+  using Sh = GemmShape<kWM, kWN>;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[Sh::kS * Sh::kSB];
+  modgemm_tile<kDeep, kWM, kWN>(g, lds, gemm_item(g));
 }
 
 // 256-column tiles, except that the last tile column holds at most 128
@@ -1329,13 +1367,13 @@ modgemm_kernel(GemmArgs g) {
 // (half the MFMA work of a 256-column tile of mostly padding).
 __global__ void __launch_bounds__(kThreads, 1)
 modgemm_mixed_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) int8_t lds[GemmShape<8>::kS * GemmShape<8>::kSB];
+  __shared__ __attribute__((aligned(1024))) int8_t lds[GemmShape<8, 8>::kS * GemmShape<8, 8>::kSB];
   GemmItem it = gemm_item(g);
   if (it.nt == g.TN - 1) {
     it.nt *= 2;
-    modgemm_tile<false, 4>(g, lds, it);
+    modgemm_tile<false, 8, 4>(g, lds, it);
   } else {
-    modgemm_tile<false, 8>(g, lds, it);
+    modgemm_tile<false, 8, 8>(g, lds, it);
   }
 }
 
@@ -1918,11 +1956,12 @@ int run(const Call& c) {
   // Shallow products with many groups run the narrow kernel (two groups per
   // CU); its column tiles past N hold only padding and are not launched.
   const bool narrow = L.gemm_tile_cols == 128;
+  const bool small = narrow && L.gemm_tile_rows == 128;
   // Wide tiles whose last tile column holds at most 128 columns of N: that
   // column runs 128-column tiles in the same launch.
   const bool mixed = !narrow && !L.deep && L.Np / kTileR >= 2 && c.N % kTileR != 0 &&
                      c.N % kTileR <= 128;
-  ga.TM = (int)(L.chunk_rows / kTileR);
+  ga.TM = small ? (int)((c.M + 127) / 128) : (int)(L.chunk_rows / kTileR);
   ga.TN = narrow ? (int)((c.N + 127) / 128) : (int)(L.Np / kTileR);
   ga.NB = L.Np / 64;
   ga.P = c.P; ga.ncorr = L.ncorr; ga.nslots = c.P + L.ncorr; ga.batch = (int)c.batch;
@@ -1962,13 +2001,15 @@ int run(const Call& c) {
       ga.nkt = (int)nkt;
       ga.first = seg == 0 ? 1 : 0;
       if (L.deep)
-        hipLaunchKernelGGL((modgemm_kernel<true, 8>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+        hipLaunchKernelGGL((modgemm_kernel<true, 8, 8>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+      else if (small)
+        hipLaunchKernelGGL((modgemm_kernel<false, 4, 4>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       else if (narrow)
-        hipLaunchKernelGGL((modgemm_kernel<false, 4>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+        hipLaunchKernelGGL((modgemm_kernel<false, 8, 4>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       else if (mixed)
         hipLaunchKernelGGL(modgemm_mixed_kernel, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       else
-        hipLaunchKernelGGL((modgemm_kernel<false, 8>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+        hipLaunchKernelGGL((modgemm_kernel<false, 8, 8>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       for (int t = 0; t < c.P && !L.deep; ++t) {
         if ((tab.p[t] & 1) || tab.p[t] == 256) continue;
         const int64_t np = (int64_t)L.ksplit * c.batch;

@@ -154,7 +154,10 @@ typedef struct {
   size_t off_sftA, off_sftB, off_lgA, off_lgB, off_bits, off_pmax, off_pss;
   size_t off_planesA, off_planesB, off_res8, off_corr, total;
   int gemm_tile_cols;       /* columns of one modular-GEMM output tile: 256, or 128 for
-                               shallow products with many tiles (two work groups per CU) */
+                               shallow products with many tiles (two work groups per CU)
+                               or where 128 columns cover N with less padding */
+  int gemm_tile_rows;       /* rows of one modular-GEMM output tile: 256, or 128 when
+                               128-row tiles cover M with less padding too */
 } fp64emu_layout_t;
 
 int fp64emu_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int nprimes, int use_corr,

@@ -288,3 +288,25 @@ def test_mixed_tile_parity(dev, kind, batch, M, N, K):
         A = _randn((M, K), seed, dev)
         B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
     check_call(kind, A, B, O.PRIMES[:14])
+
+
+@pytest.mark.parametrize("kind,batch,M,N,K", [
+    ("mm_nt", 1, 128, 128, 4096),     # c1: one 128 x 128 tile, K-split 8
+    ("bmm", 3, 100, 77, 333),         # batched, ragged
+    ("mm", 1, 300, 520, 200),         # 3 x 5 tiles of 128 x 128
+])
+def test_small_tile_parity(dev, kind, batch, M, N, K):
+    """128 x 128 GEMM tiles where both 128-row and 128-column tiles cut the
+    padded work: every stage against the oracle."""
+    from fp64_emu import capi
+    print(f"case small tiles {kind} b={batch} {M}x{N}x{K}", flush=True)
+    L = capi.layout(batch, M, N, K, 14, True)
+    assert L.gemm_tile_rows == 128 and L.gemm_tile_cols == 128
+    seed = 1300 + M + N + K
+    if kind == "bmm":
+        A = _randn((batch, M, K), seed, dev)
+        B = _randn((batch, N, K), seed + 1, dev)
+    else:
+        A = _randn((M, K), seed, dev)
+        B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
+    check_call(kind, A, B, O.PRIMES[:14])
