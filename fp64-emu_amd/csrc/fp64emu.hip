@@ -229,10 +229,22 @@ bool use_narrow_gemm(const fp64emu_layout_t& L) {
   if (L.deep) return false;
   const int64_t cols128 = (L.N + 127) / 128 * 128;
   if (cols128 * 11 < L.Np * 10) return true;
-  if (L.ksplit != 1 || L.Kp / kTileK > kNarrowMaxSteps) return false;
+  if (L.ksplit != 1 || L.Kp / kTileK > kNarrowMaxSteps || L.nprimes >= 2) return false;
   const int64_t groups = (int64_t)(L.nprimes + L.ncorr) * L.batch * (L.chunk_rows / kTileR) *
                          (cols128 / 128);
   return groups >= 2 * kCUs;
+}
+
+// Slot runs: a shallow product's groups (at most kNarrowMaxSteps k-steps per
+// slot, no K-split) each run all residue slots of their tile back to back, so
+// the operand copies stream across slots instead of every short group waiting
+// for its first stage.  Not for tiles of the mixed launch (a last tile column
+// of at most 128 columns under 256-column tiles).
+bool use_slot_runs(const fp64emu_layout_t& L) {
+  if (L.deep || L.ksplit != 1 || L.nprimes < 2 || L.Kp / kTileK > kNarrowMaxSteps) return false;
+  const bool mixed = L.gemm_tile_cols == 256 && L.Np / kTileR >= 2 && L.N % kTileR != 0 &&
+                     L.N % kTileR <= 128;
+  return !mixed;
 }
 
 // nchunk_req > 1 (batch 1, not K-segmented): the planes of A and the output
@@ -294,6 +306,7 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   const int64_t rows128 = (std::max<int64_t>(M, 1) + 127) / 128 * 128;
   L->gemm_tile_rows = (L->gemm_tile_cols == 128 && L->nchunk == 1 && rows128 * 11 < L->Mp * 10)
                           ? 128 : 256;
+  L->gemm_run = use_slot_runs(*L) ? P : 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -904,6 +917,7 @@ struct GemmArgs {
   int64_t NB;          // 64-column output blocks per output row: Np / 64
   int P, ncorr, nslots, batch;
   int ksplit;          // groups per output tile, each over a contiguous K range
+  int run;             // residue slots per group (1, or P: one slot run per tile)
   int p[kMaxP];
   double invp[kMaxP];
 };
@@ -990,8 +1004,12 @@ struct GemmShape {
 // 32x .. 32x+31, an 8x4 block of tiles sharing 12 operand panels in that
 // XCD's L2, while all XCDs work on the same slot (whose planes then stay
 // resident in the MALL).
+//
+// With slot runs (g.run > 1) the slot index counts the correction slots, then
+// one run of g.run residue slots per tile: a group runs the run's slots
+// back to back (nrun of them) on one stream of operand copies.
 struct GemmItem {
-  int split, slot, mt, nt;
+  int split, slot, nrun, mt, nt;
   int64_t b;
 };
 
@@ -1005,8 +1023,15 @@ __device__ __forceinline__ GemmItem gemm_item(const GemmArgs& g) {
   GemmItem it;
   it.split = (int)(sbs % g.ksplit);
   const int64_t sb = sbs / g.ksplit;
-  it.slot = (int)(sb / g.batch);
-  it.b = sb - (int64_t)it.slot * g.batch;
+  const int v = (int)(sb / g.batch);
+  it.b = sb - (int64_t)v * g.batch;
+  if (v < g.ncorr) {
+    it.slot = v;
+    it.nrun = 1;
+  } else {
+    it.slot = g.ncorr + (v - g.ncorr) * g.run;
+    it.nrun = min(g.run, g.nslots - it.slot);
+  }
   // Grouped tile order: 8 row tiles per group, column-major inside.
   const int GM = 8;
   const int grp = tile / (GM * g.TN);
@@ -1018,12 +1043,42 @@ __device__ __forceinline__ GemmItem gemm_item(const GemmArgs& g) {
   return it;
 }
 
-// One output tile of one slot: the body of the GEMM kernels, on the group's
-// LDS ring `lds` (the kernel's single LDS object).
-template <bool kDeep, int kWM, int kWN>
+// Balanced residues of one 16 x 64 output block of the accumulators (row
+// block x, column block h of this wave's tile) to `dst` (16 bytes per lane),
+// for slot runs.  Stage by stage over the block's 16 values, so that no
+// dependent chain is exposed.
+template <int kWM, int kWN>
+__device__ __forceinline__ void store_residue_block(const v4i (&acc)[kWM][kWN], const int x, const int h,
+                                                    const double ip, const int negp, int8_t* dst) {
+  int av[16], qv[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) av[v] = acc_read(acc[x][4 * h + v / 4][v % 4]);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int v = 0; v < 16; ++v) qv[v] = __double2loint(fma((double)av[v], ip, kMagic));
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t w[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    w[q] = pack_bytes(__mul24(qv[4 * q], negp) + av[4 * q], __mul24(qv[4 * q + 1], negp) + av[4 * q + 1],
+                      __mul24(qv[4 * q + 2], negp) + av[4 * q + 2], __mul24(qv[4 * q + 3], negp) + av[4 * q + 3]);
+  *reinterpret_cast<v4i*>(dst) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+}
+
+// One output tile of one slot (kRun: of it.nrun consecutive residue slots):
+// the body of the GEMM kernels, on the group's LDS ring `lds` (the kernel's
+// single LDS object).
+template <bool kDeep, int kWM, int kWN, bool kRun = false>
 __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, const GemmItem it) {
   using Sh = GemmShape<kWM, kWN>;
-  constexpr int kS = Sh::kS, kSB = Sh::kSB, kDma = Sh::kDma, kHB = Sh::kHB;
+  constexpr int kSB = Sh::kSB, kDma = Sh::kDma, kHB = Sh::kHB;
+  // LDS ring stages and the prefetch distance: stage kt + kPF is copied
+  // during k-step kt, into the ring slot of a stage whose fragments every
+  // wave has read (a step earlier; the step's wait and barrier retire those
+  // reads), so kPF may be as large as kS.  (A five-stage ring with four
+  // stages in flight measured no faster on shallow products, whose planes
+  // come from HBM.)
+  constexpr int kS = Sh::kS, kPF = 3;
   constexpr int kAB = Sh::kABytes;
   const int split = it.split, slot = it.slot, mt = it.mt, nt = it.nt;
   const int64_t b = it.b;
@@ -1059,13 +1114,17 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   // the LDS address alike.
   const uint32_t goff = (uint32_t)(wave * (kWM / 2) * 1024 + lane * 16);
   const uint32_t goffB = (uint32_t)(wave * (kWN / 2) * 1024 + lane * 16);
+  // kRun: the source tiles of the stage being copied, set before its copies
+  // (the k-step stream crosses from one slot's planes to the next).
+  const int8_t* cpA = At;
+  const int8_t* cpB = Bt;
 #define FP64EMU_SLOT(kt) ((kS == 4) ? ((kt) & 3) : ((kt) % kS))
 #define FP64EMU_COPY_A(kt, j)                                                               \
-  __builtin_amdgcn_global_load_lds(At + (int64_t)(kt) * kTileBytes + goff,                  \
+  __builtin_amdgcn_global_load_lds((kRun ? cpA : At + (int64_t)(kt) * kTileBytes) + goff,   \
                                    (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + wave * (kWM / 2) * 1024), \
                                    16, (j) * 1024, 0)
 #define FP64EMU_COPY_B(kt, j)                                                               \
-  __builtin_amdgcn_global_load_lds(Bt + (int64_t)(kt) * kTileBytes + goffB,                 \
+  __builtin_amdgcn_global_load_lds((kRun ? cpB : Bt + (int64_t)(kt) * kTileBytes) + goffB,  \
                                    (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + kAB +           \
                                              wave * (kWN / 2) * 1024),                      \
                                    16, (j) * 1024, 0)
@@ -1104,9 +1163,9 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   // and guarantees every wave finished reading the stage refilled next.
 #define FP64EMU_STEP(kt, FC, FN, MMA)                                                    \
   do {                                                                                   \
-    if ((kt) + 3 <= nk) wait_vm_lgkm0<kDma>(); else wait_vm_lgkm0<0>();                  \
+    if ((kt) + kPF <= nk) wait_vm_lgkm0<(kPF - 2) * kDma>(); else wait_vm_lgkm0<0>();     \
     barrier_lds();                                                                       \
-    if ((kt) + 3 < nk) FP64EMU_ISSUE((kt) + 3);                                          \
+    if ((kt) + kPF < nk) FP64EMU_ISSUE((kt) + kPF);                                      \
     FP64EMU_READF(FN, (kt) + 1);                                                         \
     FP64EMU_MMA(FC, MMA);                                                                \
   } while (0)
@@ -1134,10 +1193,10 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     const v4i* sa_ = reinterpret_cast<const v4i*>(lds + FP64EMU_SLOT((kt) + 1) * kSB);      \
     const v4i* sb_ = sa_ + kTileBytes / 16;                                                  \
     _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                          \
-      if (j == 0 && ((c) >> 1) == 0) FP64EMU_COPY_A((kt) + 3, ((c) & 1) * 2);                \
-      if (j == 2 && ((c) >> 1) == 0) FP64EMU_COPY_A((kt) + 3, ((c) & 1) * 2 + 1);            \
-      if (j == 0 && ((c) >> 1) == 1) FP64EMU_COPY_B((kt) + 3, ((c) & 1) * 2);                \
-      if (j == 2 && ((c) >> 1) == 1) FP64EMU_COPY_B((kt) + 3, ((c) & 1) * 2 + 1);            \
+      if (j == 0 && ((c) >> 1) == 0) FP64EMU_COPY_A((kt) + kPF, ((c) & 1) * 2);                \
+      if (j == 2 && ((c) >> 1) == 0) FP64EMU_COPY_A((kt) + kPF, ((c) & 1) * 2 + 1);            \
+      if (j == 0 && ((c) >> 1) == 1) FP64EMU_COPY_B((kt) + kPF, ((c) & 1) * 2);                \
+      if (j == 2 && ((c) >> 1) == 1) FP64EMU_COPY_B((kt) + kPF, ((c) & 1) * 2 + 1);            \
       __builtin_amdgcn_sched_barrier(0);                                                     \
       const int f_ = (c) * 4 + j;                                                            \
       if (f_ < 8) FN[8 + f_] = sb_[(wn * 8 + f_) * 64 + lane];                               \
@@ -1155,11 +1214,11 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     const v4i* sa_ = reinterpret_cast<const v4i*>(lds + FP64EMU_SLOT((kt) + 1) * kSB);      \
     const v4i* sb_ = sa_ + kTileBytes / 16;                                                  \
     _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                          \
-      if (j == 0 && (c) <= 1) FP64EMU_COPY_A((kt) + 3, (c) * 2);                             \
-      if (j == 2 && (c) == 0) FP64EMU_COPY_A((kt) + 3, 1);                                   \
-      if (j == 0 && (c) == 2) FP64EMU_COPY_A((kt) + 3, 3);                                   \
-      if (j == 2 && (c) == 2) FP64EMU_COPY_B((kt) + 3, 0);                                   \
-      if (j == 0 && (c) == 3) FP64EMU_COPY_B((kt) + 3, 1);                                   \
+      if (j == 0 && (c) <= 1) FP64EMU_COPY_A((kt) + kPF, (c) * 2);                             \
+      if (j == 2 && (c) == 0) FP64EMU_COPY_A((kt) + kPF, 1);                                   \
+      if (j == 0 && (c) == 2) FP64EMU_COPY_A((kt) + kPF, 3);                                   \
+      if (j == 2 && (c) == 2) FP64EMU_COPY_B((kt) + kPF, 0);                                   \
+      if (j == 0 && (c) == 3) FP64EMU_COPY_B((kt) + kPF, 1);                                   \
       __builtin_amdgcn_sched_barrier(0);                                                     \
       if (j < 3) {                                                                           \
         const int f_ = (c) * 3 + j;                                                          \
@@ -1181,8 +1240,8 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   do {                                                                                       \
     const v4i* sa_ = reinterpret_cast<const v4i*>(lds + FP64EMU_SLOT((kt) + 1) * kSB);      \
     const v4i* sb_ = sa_ + kAB / 16;                                                         \
-    if constexpr ((c) <= 1) FP64EMU_COPY_A((kt) + 3, (c));                                   \
-    else FP64EMU_COPY_B((kt) + 3, (c) - 2);                                                  \
+    if constexpr ((c) <= 1) FP64EMU_COPY_A((kt) + kPF, (c));                                   \
+    else FP64EMU_COPY_B((kt) + kPF, (c) - 2);                                                  \
     _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                          \
       __builtin_amdgcn_sched_barrier(0);                                                     \
       const int f_ = (c) * 2 + j;                                                            \
@@ -1195,7 +1254,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   } while (0)
 #define FP64EMU_STEP_FULL(kt, FC, FN, MMA)                                                   \
   do {                                                                                       \
-    wait_vm_lgkm0<kDma>();                                                                   \
+    wait_vm_lgkm0<(kPF - 2) * kDma>();                                                       \
     barrier_lds();                                                                           \
     FP64EMU_CHUNK(kt, FC, FN, 0, MMA);                                                       \
     FP64EMU_CHUNK(kt, FC, FN, 1, MMA);                                                       \
@@ -1204,7 +1263,87 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   } while (0)
 
   v4i acc[kWM][kWN];
-  if (nk == 0) {
+  // Outputs are blocks of 16 rows x 64 columns; this wave's 16 kWM x 16 kWN
+  // holds kWM row blocks x kWN/4 column blocks.  Element 16 l + 4 q + v of a
+  // block is lane l's value v of accumulator column block q (row
+  // 4 (l / 16) + v, column 16 q + l % 16).
+  if constexpr (kRun) {
+    const int64_t NB = g.NB;
+    const int64_t rb0 = (int64_t)mt * (2 * kWM) + wm * kWM, cb0 = (int64_t)nt * (kWN / 2) + wn * kHB;
+    // Residue slots slot .. slot + nrun - 1 (planes one stride apart, nk
+    // k-steps each) as one stream of nrun nk k-steps: the copies run ahead
+    // across slot boundaries, so only the first slot waits for its operands;
+    // each slot's first k-step starts the accumulators and its last one is
+    // followed by that slot's residue stores.  The first k-step after the
+    // stores waits for them too (they count in the same vector-memory counter
+    // as the copies), which is safe whatever their completion order.
+    const int nks = nk, nkr = it.nrun * nk;
+    int cj = 0, ckt = 0;   // the next stage to copy: slot cj of the run, k-step ckt
+    auto next_src = [&]() {
+      cpA = At + (int64_t)cj * g.planeA + (int64_t)ckt * kTileBytes;
+      cpB = Bt + (int64_t)cj * g.planeB + (int64_t)ckt * kTileBytes;
+      if (++ckt == nks) { ckt = 0; ++cj; }
+    };
+    auto store_slot = [&](const int s_) {
+      const int t = s_ - g.ncorr;
+      const double ip = g.invp[t];
+      const int negp = -g.p[t];
+      int8_t* rdst = g.res8 + (b * g.P + t) * g.outplane;
+#pragma unroll
+      for (int x = 0; x < kWM; ++x)
+#pragma unroll
+        for (int h = 0; h < kHB; ++h) {
+          store_residue_block<kWM, kWN>(acc, x, h, ip, negp,
+                                        rdst + ((rb0 + x) * NB + cb0 + h) * 1024 + lane * 16);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    {
+      const int nk = nkr;   // the STEP macros' end of stream
+      // A k-step G of the stream; its copy (stage G + kPF) exists while G + kPF < nk.
+#define FP64EMU_RSTEP(G, FC, FN, MMA)                                                       \
+  do {                                                                                      \
+    if ((G) + kPF < nk) next_src();                                                         \
+    FP64EMU_STEP(G, FC, FN, MMA);                                                           \
+  } while (0)
+#define FP64EMU_RSTEP_FULL(G, FC, FN)                                                       \
+  do {                                                                                      \
+    next_src();                                                                             \
+    FP64EMU_STEP_FULL(G, FC, FN, mma16);                                                    \
+  } while (0)
+#pragma unroll
+      for (int s = 0; s < kPF; ++s)
+        if (s < nk) { next_src(); FP64EMU_ISSUE(s); }
+      wait_vm_lgkm0<0>();
+      barrier_lds();
+      for (int j = 0; j < it.nrun; ++j) {
+        // Slot j: k-steps G0 .. G0 + nks - 1.  Its first stage has landed
+        // and is visible (the wait and barrier of the stream's previous
+        // step), and no copy targets it before this slot's first step.
+        const int G0 = j * nks;
+        v4i F0[kWM + kWN], F1[kWM + kWN];
+        FP64EMU_READF(F0, G0);
+        FP64EMU_RSTEP(G0, F0, F1, mma16_init);
+        int kt = 1;
+        const int kf = nk - kPF - G0;   // steps kt < kf copy stage G0 + kt + kPF
+        for (; kt + 2 <= nks && kt + 1 < kf; kt += 2) {
+          FP64EMU_RSTEP_FULL(G0 + kt, F1, F0);
+          FP64EMU_RSTEP_FULL(G0 + kt + 1, F0, F1);
+        }
+        for (; kt + 2 <= nks; kt += 2) {
+          FP64EMU_RSTEP(G0 + kt, F1, F0, mma16);
+          FP64EMU_RSTEP(G0 + kt + 1, F0, F1, mma16);
+        }
+        if (kt < nks) FP64EMU_RSTEP(G0 + kt, F1, F0, mma16);
+        mfma_fence();
+        store_slot(slot + j);
+      }
+#undef FP64EMU_RSTEP
+#undef FP64EMU_RSTEP_FULL
+      // No copy or store may still be in flight when the group retires.
+      wait_vm_lgkm0<0>();
+    }
+  } else if (nk == 0) {
     // A trailing K-split group past the end: its outputs are zeros.
 #pragma unroll
     for (int x = 0; x < kWM; ++x)
@@ -1212,7 +1351,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
       for (int y = 0; y < kWN; ++y) acc[x][y] = v4i{0, 0, 0, 0};
   } else {
 #pragma unroll
-    for (int s = 0; s < 3; ++s)
+    for (int s = 0; s < kPF; ++s)
       if (s < nk) FP64EMU_ISSUE(s);
     v4i F0[kWM + kWN], F1[kWM + kWN];
     wait_vm_lgkm0<0>();
@@ -1224,7 +1363,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     if (nk >= 4) FP64EMU_STEP_FULL(0, F0, F1, mma16_init);
     else FP64EMU_STEP(0, F0, F1, mma16_init);
     int kt = 1;
-    for (; kt + 2 <= nk - 3; kt += 2) {      // copies for kt + 3 and kt + 4 exist
+    for (; kt + 2 <= nk - kPF; kt += 2) {    // copies for kt + kPF and kt + kPF + 1 exist
       FP64EMU_STEP_FULL(kt, F1, F0, mma16);
       FP64EMU_STEP_FULL(kt + 1, F0, F1, mma16);
     }
@@ -1253,13 +1392,11 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
 #undef FP64EMU_COPY_B
 #undef FP64EMU_SLOT
 
-  // Epilogue: output blocks of 16 rows x 64 columns; this wave's 16 kWM x
-  // 16 kWN holds kWM row blocks x kWN/4 column blocks.  Element 16 l + 4 q + v
-  // of a block is lane l's value v of accumulator column block q (row
-  // 4 (l / 16) + v, column 16 q + l % 16).
+  // Epilogue (of a single slot; a run stores each slot as it ends).
   const int64_t NB = g.NB;
   const int64_t rb0 = (int64_t)mt * (2 * kWM) + wm * kWM, cb0 = (int64_t)nt * (kWN / 2) + wn * kHB;
-  if (kDeep && is_corr) {
+  if constexpr (kRun) {
+  } else if (kDeep && is_corr) {
     // K-segmented: this segment's correction products join the int64 sum.
     typedef long long v2l __attribute__((ext_vector_type(2)));
     int64_t* dst = g.cacc + b * g.outplane;
@@ -1334,7 +1471,9 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
                        acc_read(acc[x][4 * h + q][2]), acc_read(acc[x][4 * h + q][3])};
         } else {
           // Stage by stage over the block's 16 values: with one wave per
-          // SIMD nothing else hides the latency of a dependent chain.
+          // SIMD nothing else hides the latency of a dependent chain.  (The
+          // same steps as store_residue_block; written out here, where a
+          // call by reference made the compiler shuffle accumulators.)
           int av[16], qv[16];
 #pragma unroll
           for (int v = 0; v < 16; ++v) av[v] = acc_read(acc[x][4 * h + v / 4][v % 4]);
@@ -1354,12 +1493,19 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   }
 }
 
-template <bool kDeep, int kWM, int kWN>
+template <bool kDeep, int kWM, int kWN, bool kRun = false>
 __global__ void __launch_bounds__(kThreads, (kWM == 8 && kWN == 8) ? 1 : 2)
 modgemm_kernel(GemmArgs g) {
   using Sh = GemmShape<kWM, kWN>;
   __shared__ __attribute__((aligned(1024))) int8_t lds[Sh::kS * Sh::kSB];
-  modgemm_tile<kDeep, kWM, kWN>(g, lds, gemm_item(g));
+  const GemmItem it = gemm_item(g);
+  if constexpr (kRun) {
+    if (it.nrun > 1) {
+      modgemm_tile<false, kWM, kWN, true>(g, lds, it);
+      return;
+    }
+  }
+  modgemm_tile<kDeep, kWM, kWN>(g, lds, it);
 }
 
 // 256-column tiles, except that the last tile column holds at most 128
@@ -1966,8 +2112,11 @@ int run(const Call& c) {
   ga.NB = L.Np / 64;
   ga.P = c.P; ga.ncorr = L.ncorr; ga.nslots = c.P + L.ncorr; ga.batch = (int)c.batch;
   ga.ksplit = L.ksplit;
+  ga.run = L.gemm_run;
   for (int t = 0; t < kMaxP; ++t) { ga.p[t] = tab.p[t]; ga.invp[t] = tab.invp[t]; }
-  ga.total = (int64_t)ga.nslots * c.batch * L.ksplit * ga.TM * ga.TN;
+  // Work items per tile: the correction slots, then the residue slots in runs.
+  const int64_t vslots = L.ncorr + (c.P + ga.run - 1) / ga.run;
+  ga.total = vslots * c.batch * L.ksplit * ga.TM * ga.TN;
   for (int ci = 0; ci < L.nchunk; ++ci) {
     const int64_t m0 = (int64_t)ci * L.chunk_rows;              // 0 unless chunked (batch 1)
     const int64_t Mc = std::min<int64_t>(L.chunk_rows, c.M - m0);
@@ -2002,6 +2151,12 @@ int run(const Call& c) {
       ga.first = seg == 0 ? 1 : 0;
       if (L.deep)
         hipLaunchKernelGGL((modgemm_kernel<true, 8, 8>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+      else if (ga.run > 1 && small)
+        hipLaunchKernelGGL((modgemm_kernel<false, 4, 4, true>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+      else if (ga.run > 1 && narrow)
+        hipLaunchKernelGGL((modgemm_kernel<false, 8, 4, true>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+      else if (ga.run > 1)
+        hipLaunchKernelGGL((modgemm_kernel<false, 8, 8, true>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       else if (small)
         hipLaunchKernelGGL((modgemm_kernel<false, 4, 4>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       else if (narrow)

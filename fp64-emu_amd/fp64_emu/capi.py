@@ -38,7 +38,8 @@ class Layout(ctypes.Structure):
                    (n, ctypes.c_size_t) for n in (
                        "off_sftA", "off_sftB", "off_lgA", "off_lgB", "off_bits", "off_pmax",
                        "off_pss", "off_planesA", "off_planesB", "off_res8", "off_corr", "total")] + [
-                   ("gemm_tile_cols", ctypes.c_int), ("gemm_tile_rows", ctypes.c_int)]
+                   ("gemm_tile_cols", ctypes.c_int), ("gemm_tile_rows", ctypes.c_int),
+                   ("gemm_run", ctypes.c_int)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}

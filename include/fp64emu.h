@@ -158,6 +158,9 @@ typedef struct {
                                or where 128 columns cover N with less padding */
   int gemm_tile_rows;       /* rows of one modular-GEMM output tile: 256, or 128 when
                                128-row tiles cover M with less padding too */
+  int gemm_run;             /* residue slots one modular-GEMM work group runs back to back
+                               for its tile: nprimes for shallow products (at most 16
+                               k-steps, no K-split), otherwise 1 */
 } fp64emu_layout_t;
 
 int fp64emu_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int nprimes, int use_corr,

@@ -240,3 +240,13 @@ def test_minimum_workspace(shape):
         assert 0 < wmin < full
     else:
         assert wmin == full
+
+
+def test_slot_runs_only_for_shallow_products():
+    """Runs are chosen from the shapes alone: shallow products without a
+    K-split; deep, K-split and mixed-tile launches keep one slot per group."""
+    assert capi.layout(64, 512, 512, 512, 14, True).gemm_run == 14        # c4
+    assert capi.layout(1, 8192, 8192, 8192, 14, True).gemm_run == 1       # c2: 128 k-steps
+    assert capi.layout(1, 128, 128, 4096, 14, True).gemm_run == 1         # c1: K-split
+    assert capi.layout(1, 300, 1290, 200, 14, True).gemm_run == 1         # mixed tiles
+    assert capi.layout(1, 500, 500, 1024, 1, True).gemm_run == 1          # one modulus

@@ -140,7 +140,8 @@ def test_deep_k_parity(dev, kind, batch, M, N, K, P, corr, exact):
 
 
 @pytest.mark.parametrize("kind,M,N,K", [("mm_nt", 1000, 700, 3000), ("mm", 777, 300, 1500),
-                                        ("mm_nt", 2000, 100, 4096)])
+                                        ("mm_nt", 2000, 100, 4096),
+                                        ("mm_nt", 1300, 900, 700)])   # shallow: slot runs
 def test_row_chunks_match_full(dev, kind, M, N, K):
     """A workspace below the full size runs the rows of A in chunks against
     one extraction of B; the output is bit-identical to the full run, at
@@ -246,15 +247,17 @@ NARROW_CASES = [
     ("bmm", 6, 300, 260, 200, O.PRIMES[:14], True),        # 4 (corr 8), three column tiles
     ("bmm", 8, 260, 300, 1000, O.PRIMES[:14], True),       # 16 (corr 32), steady loop
     ("mm_nt", 1, 1536, 1100, 700, O.PRIMES[:15], True),    # 11, odd step count
-    ("bmm_nt", 20, 256, 256, 320, O.PRIMES[:13], False),   # 5, no correction
+    ("bmm_nt", 20, 256, 380, 320, O.PRIMES[:13], False),   # 5, no correction
+    ("mm_nt", 1, 1536, 1100, 2000, O.PRIMES[:14], True),   # 32: one slot per group
     ("bmm", 40, 64, 64, 128, MODULI_ORDERS[1], True),      # 2, even modulus 254 (tie fix)
 ]
 
 
 @pytest.mark.parametrize("kind,batch,M,N,K,primes,corr", NARROW_CASES)
 def test_narrow_tile_parity(dev, kind, batch, M, N, K, primes, corr):
-    """Shallow products with many output tiles run the 256 x 128-tile GEMM
-    (two work groups per CU): every stage against the oracle."""
+    """Products whose 256-column tiles would be mostly padding run 128-column
+    tiles (two work groups per CU; shallow ones as slot runs): every stage
+    against the oracle."""
     from fp64_emu import capi
     print(f"case narrow GEMM {kind} b={batch} {M}x{N}x{K} P={len(primes)} corr={corr}", flush=True)
     assert capi.layout(batch, M, N, K, len(primes), corr).gemm_tile_cols == 128
@@ -310,3 +313,40 @@ def test_small_tile_parity(dev, kind, batch, M, N, K):
         A = _randn((M, K), seed, dev)
         B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
     check_call(kind, A, B, O.PRIMES[:14])
+
+
+RUN_CASES = [
+    # kind, batch, M, N, K, moduli, corr, tile (rows, cols) -- k-steps per slot in the comment
+    ("bmm_nt", 3, 300, 200, 256, O.PRIMES[:14], True, (256, 256)),   # 4, wide tiles
+    ("bmm", 8, 512, 300, 1000, O.PRIMES[:14], True, (256, 128)),     # 16, narrow tiles
+    ("bmm", 5, 100, 90, 320, O.PRIMES[:14], True, (128, 128)),       # 5, small tiles
+    ("bmm_nt", 6, 100, 300, 50, O.PRIMES[:2], True, None),           # 1, a run of two slots
+    ("mm", 1, 700, 900, 150, O.PRIMES[:13], False, None),            # 3, odd stream of 39 steps
+    ("mm_nt", 1, 300, 256, 960, O.PRIMES[:20], True, None),          # 15, every modulus
+    ("bmm", 4, 200, 200, 200, MODULI_ORDERS[1], True, None),         # 4, even modulus 254
+    ("bmm_nt", 40, 100, 100, 64, O.PRIMES[:14], True, (128, 128)),   # 1, one tile per member
+    ("bmm", 6, 500, 260, 200, O.PRIMES[:14], True, (256, 128)),      # 4, three column tiles
+]
+
+
+@pytest.mark.parametrize("kind,batch,M,N,K,primes,corr,tile", RUN_CASES)
+def test_slot_run_parity(dev, kind, batch, M, N, K, primes, corr, tile):
+    """Shallow products run each tile's residue slots back to back in one
+    work group (one stream of operand copies across the slots; residues
+    stored at each slot's end): every stage against the oracle."""
+    from fp64_emu import capi
+    P = len(primes)
+    print(f"case slot runs {kind} b={batch} {M}x{N}x{K} P={P} corr={corr}", flush=True)
+    L = capi.layout(batch, M, N, K, P, corr)
+    assert L.gemm_run == P and L.ksplit == 1
+    if tile is not None:
+        assert (L.gemm_tile_rows, L.gemm_tile_cols) == tile
+    seed = 1700 + batch + M + N + K + P
+    if kind in ("bmm", "bmm_nt"):
+        A = _randn((batch, M, K), seed, dev)
+        B = _randn((batch, K, N) if kind == "bmm_nt" else (batch, N, K), seed + 1, dev)
+    else:
+        A = _randn((M, K), seed, dev)
+        B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
+    check_call(kind, A, B, primes, use_corr=corr)
+
