@@ -140,7 +140,7 @@ def test_mm_nt_and_mm_layouts_agree(dev):
 
 
 @pytest.mark.parametrize("kind,M,N,K", [
-    ("mm", 128, 96, 256),          # row sizing, narrow GEMM tiles
+    ("mm", 128, 96, 256),          # row sizing, small GEMM tiles as slot runs
     ("mm_nt", 64, 1300, 20000),    # fused row/column sizing, mixed tiles, K-split
 ])
 def test_graph_capture_replays(dev, kind, M, N, K):
