@@ -240,11 +240,16 @@ bool use_narrow_gemm(const fp64emu_layout_t& L) {
 // the operand copies stream across slots instead of every short group waiting
 // for its first stage.  Not for tiles of the mixed launch (a last tile column
 // of at most 128 columns under 256-column tiles).
+// Mixed tiles: 256-column tiles whose last tile column holds at most 128
+// columns of N run that column as 128-column tiles in the same launch.
+bool use_mixed_tiles(const fp64emu_layout_t& L) {
+  return !L.deep && L.gemm_tile_cols == 256 && L.Np / kTileR >= 2 && L.N % kTileR != 0 &&
+         L.N % kTileR <= 128;
+}
+
 bool use_slot_runs(const fp64emu_layout_t& L) {
   if (L.deep || L.ksplit != 1 || L.nprimes < 2 || L.Kp / kTileK > kNarrowMaxSteps) return false;
-  const bool mixed = L.gemm_tile_cols == 256 && L.Np / kTileR >= 2 && L.N % kTileR != 0 &&
-                     L.N % kTileR <= 128;
-  return !mixed;
+  return !use_mixed_tiles(L);
 }
 
 // nchunk_req > 1 (batch 1, not K-segmented): the planes of A and the output
@@ -307,6 +312,12 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   L->gemm_tile_rows = (L->gemm_tile_cols == 128 && L->nchunk == 1 && rows128 * 11 < L->Mp * 10)
                           ? 128 : 256;
   L->gemm_run = use_slot_runs(*L) ? P : 1;
+  // Plane rows the GEMM reads: 128-row (128-column) tiles read only the
+  // first half of a 256-row plane tile past the last one holding data, so
+  // the extraction skips the all-padding half there.
+  L->ext_rowsA = L->gemm_tile_rows == 128 ? round_up(std::max<int64_t>(M, 1), 128) : L->chunk_rows;
+  L->ext_rowsB = (L->gemm_tile_cols == 128 || use_mixed_tiles(*L))
+                     ? round_up(std::max<int64_t>(N, 1), 128) : L->Np;
 }
 
 // ---------------------------------------------------------------------------
@@ -671,7 +682,7 @@ struct ExtractArgs {
   int use_corr;
   int64_t nkt;       // Kp / 64
   int64_t planeA, planeB, memberA, memberB;
-  int64_t rgA, rgB;  // 64-row groups per member: Mp / 64, Np / 64 (0: B not extracted)
+  int64_t rgA, rgB;  // 64-row groups per member the GEMM reads (0: B not extracted)
   int64_t rgA_data, rgB_data;   // those holding operand rows: ceil(M / 64), ceil(N / 64)
   const int16_t* sftA;
   const int16_t* sftB;
@@ -2105,8 +2116,7 @@ int run(const Call& c) {
   const bool small = narrow && L.gemm_tile_rows == 128;
   // Wide tiles whose last tile column holds at most 128 columns of N: that
   // column runs 128-column tiles in the same launch.
-  const bool mixed = !narrow && !L.deep && L.Np / kTileR >= 2 && c.N % kTileR != 0 &&
-                     c.N % kTileR <= 128;
+  const bool mixed = use_mixed_tiles(L);
   ga.TM = small ? (int)((c.M + 127) / 128) : (int)(L.chunk_rows / kTileR);
   ga.TN = narrow ? (int)((c.N + 127) / 128) : (int)(L.Np / kTileR);
   ga.NB = L.Np / 64;
@@ -2134,7 +2144,7 @@ int run(const Call& c) {
       ea.nkt = nkt;
       ea.planeA = L.planeA_bytes; ea.planeB = L.planeB_bytes;
       ea.memberA = L.memberA_bytes; ea.memberB = L.memberB_bytes;
-      ea.rgA = L.chunk_rows / 64; ea.rgB = with_B ? L.Np / 64 : 0;
+      ea.rgA = L.ext_rowsA / 64; ea.rgB = with_B ? L.ext_rowsB / 64 : 0;
       ea.rgA_data = (Mc + 63) / 64; ea.rgB_data = with_B ? (c.N + 63) / 64 : 0;
       ea.sftA = sftA + m0; ea.sftB = sftB; ea.bits_eff = bits_eff;
       ea.planesA = planesA; ea.planesB = planesB;

@@ -39,7 +39,8 @@ class Layout(ctypes.Structure):
                        "off_sftA", "off_sftB", "off_lgA", "off_lgB", "off_bits", "off_pmax",
                        "off_pss", "off_planesA", "off_planesB", "off_res8", "off_corr", "total")] + [
                    ("gemm_tile_cols", ctypes.c_int), ("gemm_tile_rows", ctypes.c_int),
-                   ("gemm_run", ctypes.c_int)]
+                   ("gemm_run", ctypes.c_int), ("ext_rowsA", ctypes.c_int64),
+                   ("ext_rowsB", ctypes.c_int64)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -108,9 +109,11 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def run(kind, A, B, primes, exact=True, bits=53, use_corr=True, out=None, ws=None):
+def run(kind, A, B, primes, exact=True, bits=53, use_corr=True, out=None, ws=None, fill=None):
     """Call fp64emu_{mm,mm_nt,bmm,bmm_nt} on device tensors.  Returns
-    (out, ws, layout); `ws` holds the call's intermediates afterwards."""
+    (out, ws, layout); `ws` holds the call's intermediates afterwards.  A
+    new workspace is filled with the byte `fill` first when it is given (so
+    that tests see any read of memory the call never wrote)."""
     primes = np.ascontiguousarray(np.asarray(primes, dtype=np.int32))
     P = int(primes.size)
     batched = kind in ("bmm", "bmm_nt")
@@ -124,6 +127,8 @@ def run(kind, A, B, primes, exact=True, bits=53, use_corr=True, out=None, ws=Non
     lay = layout(batch, M, N, K, P, use_corr)
     if ws is None:
         ws = torch.empty(max(int(lay.total), 1), dtype=torch.uint8, device=A.device)
+        if fill is not None:
+            ws.fill_(fill)
     if out is None:
         shape = (batch, M, N) if batched else (M, N)
         out = torch.empty(shape, dtype=torch.float64, device=A.device)

@@ -161,6 +161,11 @@ typedef struct {
   int gemm_run;             /* residue slots one modular-GEMM work group runs back to back
                                for its tile: nprimes for shallow products (at most 16
                                k-steps, no K-split), otherwise 1 */
+  int64_t ext_rowsA;        /* rows of each A plane (per member, per row chunk) that the
+                               extraction writes: the operand rows and the zero padding
+                               that GEMM tiles read (a multiple of 128, at most the padded
+                               row count); rows past it hold unspecified bytes */
+  int64_t ext_rowsB;        /* the same for B's plane rows (the columns of B^T) */
 } fp64emu_layout_t;
 
 int fp64emu_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int nprimes, int use_corr,

@@ -45,7 +45,8 @@ def oracle_sizing(A, B, b_kn, primes, bits):
 def check_call(kind, A, B, primes, exact=True, bits=53, use_corr=True, full_oracle=True):
     """A, B: device float64 tensors in the layout `kind` expects."""
     b_kn = kind in ("mm_nt", "bmm_nt")
-    out, ws, lay = capi.run(kind, A, B, primes, exact=exact, bits=bits, use_corr=use_corr)
+    out, ws, lay = capi.run(kind, A, B, primes, exact=exact, bits=bits, use_corr=use_corr,
+                            fill=0x5A)
     torch.cuda.synchronize()
     Ah, Bh = A.cpu().numpy(), B.cpu().numpy()
     primes = np.asarray(primes, dtype=np.int32)
@@ -77,10 +78,15 @@ def check_call(kind, A, B, primes, exact=True, bits=53, use_corr=True, full_orac
     assert np.array_equal(gresA, oresA), "A residue planes differ"
     assert np.array_equal(gresB, oresB), "B residue planes differ"
     M, N, K = lay.M, lay.N, lay.K
-    pad = np.ones(gresA_p.shape, bool)
+    # Padding the GEMM reads is zero; plane rows past ext_rows are never
+    # written (the workspace was filled with a nonzero pattern before the
+    # call, so a GEMM read of them would show in its outputs below).
+    pad = np.zeros(gresA_p.shape, bool)
+    pad[:, :, :lay.ext_rowsA, :] = True
     pad[:, :, :M, :K] = False
     assert not gresA_p[pad].any(), "A padding not zero"
-    pad = np.ones(gresB_p.shape, bool)
+    pad = np.zeros(gresB_p.shape, bool)
+    pad[:, :, :lay.ext_rowsB, :] = True
     pad[:, :, :N, :K] = False
     assert not gresB_p[pad].any(), "B padding not zero"
     if use_corr:
@@ -123,7 +129,8 @@ def sampled_parity(kind, A, B, primes, rows, cols, exact=True, bits=53, use_corr
     rows and columns at that sizing.  2-D kinds only.  Returns
     (out, bits_eff, workspace layout, device workspace)."""
     b_kn = kind == "mm_nt"
-    out, ws, lay = capi.run(kind, A, B, primes, exact=exact, bits=bits, use_corr=use_corr)
+    out, ws, lay = capi.run(kind, A, B, primes, exact=exact, bits=bits, use_corr=use_corr,
+                            fill=0x5A)
     torch.cuda.synchronize()
     primes = np.asarray(primes, dtype=np.int32)
     head = ws[:lay.off_planesA].cpu().numpy()

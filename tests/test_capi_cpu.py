@@ -86,6 +86,13 @@ def test_layout_consistency(shape, P, corr):
     assert L.memberA_bytes == nplanes * L.planeA_bytes
     assert L.memberB_bytes == nplanes * L.planeB_bytes
     assert L.outplane_bytes == L.Mp * L.Np
+    # Extracted plane rows: every operand row, a multiple of 128, within the
+    # padded plane; short of it only where GEMM tiles are 128 wide.
+    # (B also under mixed tiles, whose last tile column is read 128 wide.)
+    for ext, R, Rp, short_ok in ((L.ext_rowsA, M, L.chunk_rows, L.gemm_tile_rows == 128),
+                                 (L.ext_rowsB, N, L.Np, not deep)):
+        assert ext % 128 == 0 and min(max(R, 1), Rp) <= ext <= Rp
+        assert ext == Rp or (short_ok and ext == -(-max(R, 1) // 128) * 128)
     sizes = [("off_sftA", 2 * batch * M), ("off_sftB", 2 * batch * N), ("off_lgA", 4 * batch * M),
              ("off_lgB", 4 * batch * N), ("off_bits", 16), ("off_pmax", 8 * L.nslab * batch * N),
              ("off_pss", 8 * L.nslab * batch * N), ("off_planesA", batch * L.memberA_bytes),
