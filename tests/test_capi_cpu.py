@@ -257,3 +257,20 @@ def test_slot_runs_only_for_shallow_products():
     assert capi.layout(1, 128, 128, 4096, 14, True).gemm_run == 1         # c1: K-split
     assert capi.layout(1, 300, 1290, 200, 14, True).gemm_run == 1         # mixed tiles
     assert capi.layout(1, 500, 500, 1024, 1, True).gemm_run == 1          # one modulus
+
+
+def test_sweep_reaches_every_gemm_form():
+    """The GPU sweep's shapes (tests/test_gpu_sweep.py) cover each launch
+    form of the modular GEMM."""
+    from test_gpu_sweep import CASES
+    forms = set()
+    for (_, kind, batch, M, N, K, P, corr, _) in CASES:
+        L = capi.layout(batch, M, N, K, P, corr)
+        mixed = (L.gemm_tile_cols == 256 and L.Np // 256 >= 2 and 0 < N % 256 <= 128)
+        forms.add(("tile", L.gemm_tile_rows, L.gemm_tile_cols, mixed))
+        forms.add(("ksplit", L.ksplit > 1))
+        forms.add(("run", L.gemm_run > 1))
+    for f in [("tile", 256, 256, False), ("tile", 256, 256, True), ("tile", 256, 128, False),
+              ("tile", 128, 128, False), ("ksplit", True), ("ksplit", False), ("run", True),
+              ("run", False)]:
+        assert f in forms, f
