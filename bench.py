@@ -43,10 +43,15 @@ def parse():
     ap.add_argument("--configs", action="store_true",
                     help="instead of the headline line, one JSON line per BASELINE config "
                          "(c1, c2, c3a, c3b, c4, c5 default and reduced)")
+    ap.add_argument("--config", choices=CONFIG_NAMES, default=None,
+                    help="with --configs: only this config (for a profiler run)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a float64 streaming kernel over 1 GiB (read 1 GiB, write "
                          "1 GiB) three times: the scale of the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
+
+
+CONFIG_NAMES = ("c1", "c2", "c3a", "c3b", "c4", "c5", "c5r")
 
 
 def calibrate_copy():
@@ -77,7 +82,8 @@ def main():
         calibrate_copy()
         return
     if args.configs:
-        run_configs(max(args.steps, 3), max(args.warmup, 1))
+        run_configs(max(args.steps, 3), max(args.warmup, 1),
+                    [args.config] if args.config else CONFIG_NAMES)
         return
 
     import torch
@@ -243,7 +249,7 @@ def _config_inputs(name, torch):
     return "mm_nt", A, B, ((13, False) if name == "c5r" else None)
 
 
-def run_configs(steps, warmup):
+def run_configs(steps, warmup, names):
     """One JSON line per BASELINE config: effective FP64 TFLOPS, the
     plan-adjusted INT8 roofline fraction, per-phase ms (mm_nt forms), the
     native float64 comparator and correct bits against the device
@@ -252,7 +258,7 @@ def run_configs(steps, warmup):
     import fp64_emu
     from fp64_emu import capi
     dev = torch.device("cuda:0")
-    for name in ("c1", "c2", "c3a", "c3b", "c4", "c5", "c5r"):
+    for name in names:
         kind, A, B, plan = _config_inputs(name, torch)
         A, B = A.to(dev), B.to(dev)
         batched = kind == "bmm_nt"
