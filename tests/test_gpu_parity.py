@@ -27,6 +27,9 @@ CASES = [
     ("bmm", 5, 96, 64, 256, 14, True),
     ("mm", 1, 64, 48, 64, 20, True),
     ("mm_nt", 1, 64, 40, 100_000, 15, True),    # two int32 correction planes, K-split 16
+    # >= 4096 short rows (one wave per row in the sizing), odd row counts
+    ("bmm", 9, 301, 256, 300, 14, True),         # A and B rows, 5013 in all
+    ("bmm_nt", 17, 257, 100, 448, 13, True),     # A's 4369 rows beside the column slabs
 ]
 
 
