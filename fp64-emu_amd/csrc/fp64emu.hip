@@ -29,6 +29,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -2239,6 +2240,39 @@ Call make_call(double* out, const double* A, const double* B, int64_t batch, int
 }  // namespace
 
 // ---------------------------------------------------------------------------
+// Static scratch of fp64emu_mm_nt_noalloc: each GPU holds its own copy of
+// this array for the life of the process.  In host code `scratch` names a
+// host-side stand-in, not the device memory: the device address comes from
+// hipGetSymbolAddress, once per device (with that device current), and only
+// that address is ever passed to kernels.
+static __device__ __align__(256) unsigned char scratch[FP64EMU_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// The current device's address of `scratch` (looked up on its first use).
+int scratch_address(void** out) {
+  int dev = -1;
+  if (int st = check_hip(hipGetDevice(&dev), "hipGetDevice")) return st;
+  if (dev < 0 || dev >= kMaxDevices) return fail(FP64EMU_EHIP, "device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    if (int st = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress"))
+      return st;
+    if (!p) return fail(FP64EMU_EHIP, "hipGetSymbolAddress: null scratch address");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return FP64EMU_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
 // C ABI
 
 extern "C" {
@@ -2361,6 +2395,32 @@ int fp64emu_mm_nt_events(double* out, const double* A, const double* Bt, int64_t
                      workspace, workspace_bytes, stream);
   c.ev = ev;
   return run(c);
+}
+
+int fp64emu_mm_nt_noalloc(double* out, const double* A, const double* Bt, int64_t M, int64_t N,
+                          int64_t K, const int32_t* primes, const int32_t* inv,
+                          const int64_t* mu, int nprimes, int exact, int64_t bits,
+                          int use_corr, fp64emu_stream_t stream) {
+  (void)inv; (void)mu;
+  g_err.clear();
+  // Argument checks first, then the size check, both before any HIP call.
+  if (int st = validate_primes(primes, nprimes)) return st;
+  if (bits < 16 || bits > 53) return fail(FP64EMU_EINVAL, "bits must be in [16, 53]");
+  if (M < 0 || N < 0 || K < 0) return fail(FP64EMU_EINVAL, "shapes must be non-negative");
+  if (K > kMaxKSingle) return fail(FP64EMU_EINVAL, "K bound for int32 modular GEMM");
+  const size_t need = fp64emu_workspace_size_min(1, M, N, K, nprimes, use_corr);
+  if (need > FP64EMU_NOALLOC_SCRATCH_BYTES)
+    return fail(FP64EMU_EWORKSPACE,
+                "problem too large for the static scratch of fp64emu_mm_nt_noalloc: needs " +
+                    std::to_string(need) + " bytes, holds " +
+                    std::to_string((unsigned long long)FP64EMU_NOALLOC_SCRATCH_BYTES));
+  if (M == 0 || N == 0 || K == 0)   // no workspace use: the ordinary entry point's path
+    return run(make_call(out, A, Bt, 1, M, N, K, true, primes, nprimes, exact, bits, use_corr,
+                         nullptr, 0, stream));
+  void* ws = nullptr;
+  if (int st = scratch_address(&ws)) return st;
+  return run(make_call(out, A, Bt, 1, M, N, K, true, primes, nprimes, exact, bits, use_corr, ws,
+                       FP64EMU_NOALLOC_SCRATCH_BYTES, stream));
 }
 
 int fp64emu_ddgemm_nt(double* hi, double* lo, const double* A, const double* B, int64_t M,

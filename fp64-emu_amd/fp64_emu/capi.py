@@ -23,7 +23,10 @@ TILE_R, TILE_K, FRAG = 256, 64, 1024
 EXPORTS = ("fp64emu_maxp", "fp64emu_last_error", "fp64emu_workspace_size",
            "fp64emu_workspace_size_min", "fp64emu_mm",
            "fp64emu_mm_nt", "fp64emu_bmm", "fp64emu_bmm_nt", "fp64emu_mm_timed",
-           "fp64emu_mm_nt_events", "fp64emu_layout", "fp64emu_ddgemm_nt")
+           "fp64emu_mm_nt_events", "fp64emu_mm_nt_noalloc", "fp64emu_layout",
+           "fp64emu_ddgemm_nt")
+
+NOALLOC_SCRATCH_BYTES = 64 << 20   # FP64EMU_NOALLOC_SCRATCH_BYTES
 
 
 class Layout(ctypes.Structure):
@@ -74,6 +77,9 @@ def lib():
     L.fp64emu_mm_timed.restype = i32
     L.fp64emu_mm_nt_events.argtypes = mm_args + [ctypes.POINTER(ctypes.c_void_p)]
     L.fp64emu_mm_nt_events.restype = i32
+    L.fp64emu_mm_nt_noalloc.argtypes = [vp, vp, vp, i64, i64, i64, vp, vp, vp, i32, i32, i64,
+                                        i32, vp]
+    L.fp64emu_mm_nt_noalloc.restype = i32
     L.fp64emu_layout.argtypes = [i64, i64, i64, i64, i32, i32, ctypes.POINTER(Layout)]
     L.fp64emu_layout.restype = i32
     L.fp64emu_ddgemm_nt.argtypes = [vp, vp, vp, vp, i64, i64, i64, vp]
@@ -219,6 +225,21 @@ def mm_nt_events(A, Bt, primes, out, ws, events, exact=True, bits=53, use_corr=T
                                       primes.size, int(bool(exact)), int(bits),
                                       int(bool(use_corr)), ws.data_ptr(), ws.numel(), _stream(),
                                       events.handles))
+    return out
+
+
+def mm_nt_noalloc(A, Bt, primes, out=None, exact=True, bits=53, use_corr=True):
+    """fp64emu_mm_nt_noalloc: the library's static device scratch instead of
+    a workspace argument."""
+    primes = np.ascontiguousarray(np.asarray(primes, dtype=np.int32))
+    M, K = A.shape
+    N = Bt.shape[1]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float64, device=A.device)
+    _check(lib().fp64emu_mm_nt_noalloc(out.data_ptr(), A.data_ptr(), Bt.data_ptr(), M, N, K,
+                                       primes.ctypes.data_as(ctypes.c_void_p), None, None,
+                                       primes.size, int(bool(exact)), int(bits),
+                                       int(bool(use_corr)), _stream()))
     return out
 
 

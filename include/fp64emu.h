@@ -66,10 +66,13 @@ size_t fp64emu_workspace_size(int64_t batch, int64_t M, int64_t N, int64_t K,
                               int nprimes, int use_corr);
 
 /* The smallest workspace a call accepts.  With less than
- * fp64emu_workspace_size() bytes, a call with batch 1 and K <= 131071 runs
- * the rows of A in chunks of 256-row multiples against one extraction of B
- * (the fewest chunks that fit), so products too large for the full
- * workspace still run.  Other calls need the full size.  No reference
+ * fp64emu_workspace_size() bytes, a call of fp64emu_mm, fp64emu_mm_nt or
+ * fp64emu_mm_nt_noalloc with K <= 131071 runs the rows of A in chunks of
+ * 256-row multiples against one extraction of B (the fewest chunks that
+ * fit), so products too large for the full workspace still run.  Other
+ * calls (batched, K-segmented, and the phase-timed fp64emu_mm_timed and
+ * fp64emu_mm_nt_events, whose events bracket whole phases) need the full
+ * size.  No reference
  * counterpart: the reference allocates its scratch per call (README.md:105-107
  * describes chunking only for its cuBLAS engine). */
 size_t fp64emu_workspace_size_min(int64_t batch, int64_t M, int64_t N, int64_t K,
@@ -121,6 +124,26 @@ int fp64emu_mm_nt_events(double* out, const double* A, const double* Bt, int64_t
                          int nprimes, int exact, int64_t bits, int use_corr, void* workspace,
                          size_t workspace_bytes, fp64emu_stream_t stream,
                          const fp64emu_event_t* events /* host, 5 events */);
+
+/* Bytes of the static device scratch of fp64emu_mm_nt_noalloc (64 MiB). */
+#define FP64EMU_NOALLOC_SCRATCH_BYTES (64ull << 20)
+
+/* fp64emu_mm_nt without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No reference counterpart.  The
+ * scratch is a static device array of FP64EMU_NOALLOC_SCRATCH_BYTES that the
+ * library holds on every GPU it runs on until the process ends; the call
+ * itself allocates nothing.  Products whose full workspace exceeds it run
+ * the rows of A in chunks (see fp64emu_workspace_size_min); a product whose
+ * smallest workspace exceeds it is rejected with FP64EMU_EWORKSPACE before
+ * anything is enqueued.  Every call on one GPU uses that GPU's one array:
+ * calls that overlap on one GPU (other streams, other host threads) race
+ * and must be serialized by the caller.  The device of `stream` must be the
+ * current device.  Results are bit-identical to fp64emu_mm_nt. */
+int fp64emu_mm_nt_noalloc(double* out, const double* A, const double* Bt, int64_t M, int64_t N,
+                          int64_t K, const int32_t* primes, const int32_t* inv,
+                          const int64_t* mu, int nprimes, int exact, int64_t bits,
+                          int use_corr, fp64emu_stream_t stream);
 
 /* ---- Workspace map (inspection of intermediates; no reference
  * counterpart: the reference's scratch is private torch tensors).  After a

@@ -162,6 +162,28 @@ def test_validation_messages(kind):
     assert _call(kind, null_ops=True)[0] == EINVAL
 
 
+def test_noalloc_validation_before_device_work():
+    """fp64emu_mm_nt_noalloc checks its arguments and the static scratch's
+    limit before any HIP call, so the refusals show here without a GPU."""
+    L = capi.lib()
+    pr = np.asarray(capi_primes(14), dtype=np.int32)
+    pp = pr.ctypes.data_as(ctypes.c_void_p)
+
+    def call(M, N, K, P=14, bits=53, primes=pp):
+        st = L.fp64emu_mm_nt_noalloc(None, None, None, M, N, K, primes, None, None, P, 1, bits,
+                                     1, None)
+        return st, L.fp64emu_last_error().decode()
+
+    assert call(64, 64, 64, bits=15) == (EINVAL, "bits must be in [16, 53]")
+    assert call(64, 64, 131072) == (EINVAL, "K bound for int32 modular GEMM")
+    assert call(-1, 64, 64) == (EINVAL, "shapes must be non-negative")
+    st, msg = call(256, 4096, 8192)     # B's planes alone are 512 MiB
+    assert st == EWORKSPACE and "too large for the static scratch" in msg
+    need = capi.workspace_size_min(1, 256, 4096, 8192, 14, True)
+    assert str(need) in msg and need > capi.NOALLOC_SCRATCH_BYTES
+    assert call(0, 64, 64) == (0, "")   # empty: nothing to do, no device touched
+
+
 def test_empty_shapes_are_a_no_op():
     assert _call("mm_nt", M=0)[0] == 0
     assert _call("mm", N=0)[0] == 0
