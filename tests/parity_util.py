@@ -121,16 +121,21 @@ def check_call(kind, A, B, primes, exact=True, bits=53, use_corr=True, full_orac
     return out, ws, lay
 
 
-def sampled_parity(kind, A, B, primes, rows, cols, exact=True, bits=53, use_corr=True):
+def sampled_parity(kind, A, B, primes, rows, cols, exact=True, bits=53, use_corr=True,
+                   ws=None):
     """Parity at sizes the oracle cannot finish whole: run the C-ABI call,
     then check (1) the sizing (shifts, width) against the oracle's sizing of
     the full operands, and (2) the outputs at rows x cols bit-exact against
     the oracle's extraction, modular GEMMs and reconstruction of just those
-    rows and columns at that sizing.  2-D kinds only.  Returns
+    rows and columns at that sizing.  2-D kinds only.  `ws`: a caller's
+    workspace (one below the full size runs the rows of A in chunks; the
+    sizing region sits at the same offsets either way).  Returns
     (out, bits_eff, workspace layout, device workspace)."""
     b_kn = kind == "mm_nt"
+    if ws is not None:
+        ws.fill_(0x5A)
     out, ws, lay = capi.run(kind, A, B, primes, exact=exact, bits=bits, use_corr=use_corr,
-                            fill=0x5A)
+                            ws=ws, fill=0x5A)
     torch.cuda.synchronize()
     primes = np.asarray(primes, dtype=np.int32)
     head = ws[:lay.off_planesA].cpu().numpy()

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 import oracle as O
-from parity_util import check_call
+from parity_util import check_call, sampled_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -163,6 +163,13 @@ def test_row_chunks_match_full(dev, kind, M, N, K):
         out, _, _ = capi.run(kind, A, B, O.PRIMES[:P], ws=ws)
         torch.cuda.synchronize()
         assert torch.equal(out, full), f"workspace {wbytes}"
+    # The chunked run at the minimum workspace against the oracle itself, at
+    # rows across chunk boundaries (256-row multiples) and both ends.
+    ws = torch.empty(wmin, dtype=torch.uint8, device=dev)
+    rows = sorted({0, 1, 255, 256, 511, 512, M // 2, M - 2, M - 1} & set(range(M)))
+    cols = sorted({0, 1, N // 3, N - 1})
+    out, _, lay, _ = sampled_parity(kind, A, B, O.PRIMES[:P], rows, cols, ws=ws)
+    assert torch.equal(out, full)
     with pytest.raises(capi.CapiError, match="workspace too small"):
         capi.run(kind, A, B, O.PRIMES[:P], ws=torch.empty(wmin - 256, dtype=torch.uint8, device=dev))
 
