@@ -217,13 +217,15 @@ int choose_ksplit(int64_t batch, int64_t tiles, int64_t nkt, int P, int ncorr) {
 }
 
 // The narrow GEMM (256 x 128 tiles, two groups per CU):
-// - for products whose groups are short (k-steps <= kNarrowMaxSteps; the
-//   fused correction slot runs twice as many) and numerous enough to give
-//   every CU two, so that groups overlap their prologues and epilogues;
 // - for products whose 256-column tiles are mostly padding: 128-column tiles
 //   cover N with at most 127 padded columns, worth it where that cuts the
 //   MFMA work by more than the narrow loop's ~10% lower efficiency at depth
-//   (e.g. N = 128: half the work).
+//   (e.g. N = 128: half the work);
+// - for a single modulus (no slot run) whose groups are short (k-steps <=
+//   kNarrowMaxSteps; the fused correction slot runs twice as many) and
+//   numerous enough to give every CU two, so that groups overlap their
+//   prologues and epilogues.  Shallow products with two or more moduli run
+//   slot runs instead (use_slot_runs).
 constexpr int64_t kNarrowMaxSteps = 16;
 
 bool use_narrow_gemm(const fp64emu_layout_t& L) {
@@ -1286,9 +1288,14 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     // k-steps each) as one stream of nrun nk k-steps: the copies run ahead
     // across slot boundaries, so only the first slot waits for its operands;
     // each slot's first k-step starts the accumulators and its last one is
-    // followed by that slot's residue stores.  The first k-step after the
-    // stores waits for them too (they count in the same vector-memory counter
-    // as the copies), which is safe whatever their completion order.
+    // followed by that slot's residue stores.  The stores count in the same
+    // vector-memory counter as the copies, and the first k-step after them
+    // waits for the counter to fall to kDma: that proves the stage it needs
+    // (issued before the stores) has landed because gfx9-family counters
+    // retire vector-memory operations in issue order (CDNA3 ISA, "Data
+    // dependency resolution": reads and writes return in the order issued),
+    // so the count reaches kDma only after every operation older than the
+    // last kDma -- the stage and everything before it.
     const int nks = nk, nkr = it.nrun * nk;
     int cj = 0, ckt = 0;   // the next stage to copy: slot cj of the run, k-step ckt
     auto next_src = [&]() {
@@ -2048,18 +2055,6 @@ int run(const Call& c) {
     }
     if (!fits) return fail(FP64EMU_EWORKSPACE, "workspace too small");
   }
-  {
-    // A dispatch holds its grid size in work-items as 32 bits.
-    const int64_t limit = (int64_t)0xFFFFFFFFu / kThreads;
-    const int64_t nkt_max = L.Kp / kTileK;
-    const int64_t grids[4] = {
-        (MF + NF + kRowsPerBlock - 1) / kRowsPerBlock,             // row sizing
-        c.batch * (L.chunk_rows / 64 + L.Np / 64) * nkt_max,       // extraction
-        (int64_t)(c.P + L.ncorr) * c.batch * L.ksplit * (L.chunk_rows / kTileR) * (L.Np / 128),
-        c.batch * ((c.M + 31) / 32) * ((c.N + 31) / 32)};          // reconstruction
-    for (int64_t gsz : grids)
-      if (gsz > limit) return fail(FP64EMU_EINVAL, "problem too large for one launch");
-  }
   const ModTables tab = make_tables(c.primes, c.P);
   bool default_moduli = true;
   for (int t = 0; t < c.P; ++t) default_moduli = default_moduli && c.primes[t] == kDefaultModuli[t];
@@ -2076,6 +2071,48 @@ int run(const Call& c) {
   int8_t* planesB = reinterpret_cast<int8_t*>(ws + L.off_planesB);
   int8_t* res8 = reinterpret_cast<int8_t*>(ws + L.off_res8);
   int32_t* corr = reinterpret_cast<int32_t*>(ws + L.off_corr);
+
+  // The modular GEMM's arguments (its launches follow the sizing).
+  GemmArgs ga;
+  ga.A = planesA; ga.B = planesB; ga.res8 = res8; ga.corr = corr;
+  ga.racc = L.deep ? reinterpret_cast<int32_t*>(res8) : nullptr;
+  ga.cacc = L.deep ? reinterpret_cast<int64_t*>(corr) : nullptr;
+  ga.memberA = L.memberA_bytes; ga.memberB = L.memberB_bytes;
+  ga.planeA = L.planeA_bytes; ga.planeB = L.planeB_bytes;
+  ga.outplane = L.outplane_bytes;
+  // Shallow products with many groups run the narrow kernel (two groups per
+  // CU); its column tiles past N hold only padding and are not launched.
+  const bool narrow = L.gemm_tile_cols == 128;
+  const bool small = narrow && L.gemm_tile_rows == 128;
+  // Wide tiles whose last tile column holds at most 128 columns of N: that
+  // column runs 128-column tiles in the same launch.
+  const bool mixed = use_mixed_tiles(L);
+  ga.TM = small ? (int)((c.M + 127) / 128) : (int)(L.chunk_rows / kTileR);
+  ga.TN = narrow ? (int)((c.N + 127) / 128) : (int)(L.Np / kTileR);
+  ga.NB = L.Np / 64;
+  ga.P = c.P; ga.ncorr = L.ncorr; ga.nslots = c.P + L.ncorr; ga.batch = (int)c.batch;
+  ga.ksplit = L.ksplit;
+  ga.run = L.gemm_run;
+  for (int t = 0; t < kMaxP; ++t) { ga.p[t] = tab.p[t]; ga.invp[t] = tab.invp[t]; }
+  // Work items per tile: the correction slots, then the residue slots in runs.
+  const int64_t vslots = L.ncorr + (c.P + ga.run - 1) / ga.run;
+  ga.total = vslots * c.batch * L.ksplit * ga.TM * ga.TN;
+
+  {
+    // A dispatch holds its grid size in work-items as 32 bits: every launch
+    // below, sized as it will be launched, is checked before the first one.
+    const int64_t limit = (int64_t)0xFFFFFFFFu / kThreads;
+    int64_t kslab; int nslab;
+    slab_split(NF, c.K, &kslab, &nslab);
+    const int64_t sizing = !c.b_kn ? (MF + NF < kRowsGroupBelow ? MF + NF
+                                                                 : (MF + NF + kRowsPerBlock - 1) / kRowsPerBlock)
+                                   : (MF < kRowsGroupBelow ? MF : (MF + kRowsPerBlock - 1) / kRowsPerBlock) +
+                                         (NF + kThreads - 1) / kThreads * nslab;
+    const int64_t extraction = c.batch * (L.ext_rowsA / 64 + L.ext_rowsB / 64) * (L.Kp / kTileK);
+    const int64_t recon = c.batch * ((std::min<int64_t>(L.chunk_rows, c.M) + 15) / 16) * ((c.N + 63) / 64);
+    for (int64_t gsz : {sizing, extraction, ga.total, recon})
+      if (gsz > limit) return fail(FP64EMU_EINVAL, "problem too large for one launch");
+  }
 
   // 1. sizing
   if (!c.b_kn) {
@@ -2104,30 +2141,6 @@ int run(const Call& c) {
   // segment (one unless deep): extraction (covering the padded planes
   // entirely, so no memset), every modular GEMM in one launch, then the
   // reconstruction of the chunk's rows.  B's planes are extracted once.
-  GemmArgs ga;
-  ga.A = planesA; ga.B = planesB; ga.res8 = res8; ga.corr = corr;
-  ga.racc = L.deep ? reinterpret_cast<int32_t*>(res8) : nullptr;
-  ga.cacc = L.deep ? reinterpret_cast<int64_t*>(corr) : nullptr;
-  ga.memberA = L.memberA_bytes; ga.memberB = L.memberB_bytes;
-  ga.planeA = L.planeA_bytes; ga.planeB = L.planeB_bytes;
-  ga.outplane = L.outplane_bytes;
-  // Shallow products with many groups run the narrow kernel (two groups per
-  // CU); its column tiles past N hold only padding and are not launched.
-  const bool narrow = L.gemm_tile_cols == 128;
-  const bool small = narrow && L.gemm_tile_rows == 128;
-  // Wide tiles whose last tile column holds at most 128 columns of N: that
-  // column runs 128-column tiles in the same launch.
-  const bool mixed = use_mixed_tiles(L);
-  ga.TM = small ? (int)((c.M + 127) / 128) : (int)(L.chunk_rows / kTileR);
-  ga.TN = narrow ? (int)((c.N + 127) / 128) : (int)(L.Np / kTileR);
-  ga.NB = L.Np / 64;
-  ga.P = c.P; ga.ncorr = L.ncorr; ga.nslots = c.P + L.ncorr; ga.batch = (int)c.batch;
-  ga.ksplit = L.ksplit;
-  ga.run = L.gemm_run;
-  for (int t = 0; t < kMaxP; ++t) { ga.p[t] = tab.p[t]; ga.invp[t] = tab.invp[t]; }
-  // Work items per tile: the correction slots, then the residue slots in runs.
-  const int64_t vslots = L.ncorr + (c.P + ga.run - 1) / ga.run;
-  ga.total = vslots * c.batch * L.ksplit * ga.TM * ga.TN;
   for (int ci = 0; ci < L.nchunk; ++ci) {
     const int64_t m0 = (int64_t)ci * L.chunk_rows;              // 0 unless chunked (batch 1)
     const int64_t Mc = std::min<int64_t>(L.chunk_rows, c.M - m0);

@@ -176,9 +176,11 @@ typedef struct {
                                planes (deep: one int64 sum plane) */
   size_t off_sftA, off_sftB, off_lgA, off_lgB, off_bits, off_pmax, off_pss;
   size_t off_planesA, off_planesB, off_res8, off_corr, total;
-  int gemm_tile_cols;       /* columns of one modular-GEMM output tile: 256, or 128 for
-                               shallow products with many tiles (two work groups per CU)
-                               or where 128 columns cover N with less padding */
+  int gemm_tile_cols;       /* columns of one modular-GEMM output tile: 256, or 128 where
+                               128 columns cover N with less padding, or for a single
+                               modulus in shallow products with many tiles (two work
+                               groups per CU; shallow products with more moduli run
+                               slot runs) */
   int gemm_tile_rows;       /* rows of one modular-GEMM output tile: 256, or 128 when
                                128-row tiles cover M with less padding too */
   int gemm_run;             /* residue slots one modular-GEMM work group runs back to back

@@ -502,9 +502,12 @@ int or_mm(double* out, const double* A, const double* B, int64_t batch, int64_t 
   int8_t* res8 = (int8_t*)malloc(po * P + 1);
   int32_t* c1 = (int32_t*)malloc(sizeof(int32_t) * po + 4);
   int32_t* c2 = (int32_t*)malloc(sizeof(int32_t) * po + 4);
+  int rc = 0;
   if (!sftA || !sftB || !lgA || !lgB || !resA || !resB || !res8 || !c1 || !c2 ||
-      (use_corr && (!hA || !qA || !hB || !qB)))
-    return -1;
+      (use_corr && (!hA || !qA || !hB || !qB))) {
+    rc = -1;
+    goto done;
+  }
 
   or_size_rows(A, MF, K, bits, sftA, lgA);
   if (b_kn) or_size_cols(B, batch, K, N, bits, sftB, lgB);
@@ -522,8 +525,10 @@ int or_mm(double* out, const double* A, const double* B, int64_t batch, int64_t 
                        hB, qB);
     if (K > 131071 && !b_kn) {
       if (or_mm_segmented(resA, hA, qA, resB, hB, qB, M, N, K, primes, P, use_corr, nthreads, be,
-                          sftA + b * M, sftB + b * N, exact, out + b * M * N))
-        return -1;
+                          sftA + b * M, sftB + b * N, exact, out + b * M * N)) {
+        rc = -1;
+        goto done;
+      }
       continue;
     }
     for (int t = 0; t < P; t++)
@@ -535,10 +540,12 @@ int or_mm(double* out, const double* A, const double* B, int64_t batch, int64_t 
     or_reconstruct(res8, use_corr ? c1 : NULL, use_corr ? c2 : NULL, M, N, primes, P, be,
                    sftA + b * M, sftB + b * N, exact, out + b * M * N);
   }
+done:
+  /* free(NULL) is a no-op: every buffer goes, whichever allocation failed. */
   free(sftA); free(sftB); free(lgA); free(lgB); free(resA); free(resB); free(res8);
   free(c1); free(c2);
-  if (use_corr) { free(hA); free(qA); free(hB); free(qB); }
-  return 0;
+  free(hA); free(qA); free(hB); free(qB);
+  return rc;
 }
 
 /* ---- double-double reference GEMM: bench/accuracy.py:21-50 ---------------
