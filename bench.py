@@ -2,7 +2,8 @@
 the default plan, on one MI355X.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--n 8192] [--no-accuracy]
-                [--no-cpu] [--calibrate-copy]
+                [--no-cpu] [--no-configs] [--configs [--config NAME]]
+                [--accuracy-grid] [--calibrate-copy]
 
 One step = one emulated mm_nt of resident 8192x8192 float64 operands (iid
 N(0,1) from CPU seeds 2000/2001, configs[1]) through the C ABI
@@ -14,8 +15,12 @@ boundaries), the same step through the torch op fp64_emu.mm_nt, native rocBLAS
 DGEMM (torch.matmul float64 on the device) throughput, correct bits of both
 against a device double-double GEMM, the plan-adjusted INT8 roofline
 fraction, the `roofline` object for the dominant kernel (the modular GEMM,
-its duration from the events bracketing its launch in every timed call) and the CPU
-baseline (the oracle port on a bounded sample of the same workload).
+its duration from the events bracketing its launch in every timed call), the CPU
+baseline (the oracle port on a bounded sample of the same workload), torch
+float64 matmul on the host's cores, and under "configs" every other BASELINE
+config (c1, c3a, c3b, c4, c5, c5 reduced) plus c2 with the fp64 combine (c2i)
+and at the reduced plan (c2r), each with its ms, TFLOP/s, plan fraction,
+phases, native comparator and correct bits.
 """
 import argparse
 import json
@@ -26,6 +31,10 @@ import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "fp64-emu_amd"))
+
+# The native comparator is rocBLAS DGEMM: torch's float64 matmul with the
+# hipBLASLt preference off, set before torch initialises its BLAS handles.
+os.environ.setdefault("TORCH_BLAS_PREFER_HIPBLASLT", "0")
 
 INT8_PEAK_TOPS = 5000.0    # MI355X dense INT8 MFMA, 5.0 POP/s
 HBM_PEAK_GBS = 8000.0
@@ -40,18 +49,26 @@ def parse():
     ap.add_argument("--n", type=int, default=8192)
     ap.add_argument("--no-accuracy", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="leave out the per-config records (c1, c2 inexact and reduced, c3a, "
+                         "c3b, c4, c5, c5 reduced) that the headline line carries under "
+                         "\"configs\"")
     ap.add_argument("--configs", action="store_true",
                     help="instead of the headline line, one JSON line per BASELINE config "
                          "(c1, c2, c3a, c3b, c4, c5 default and reduced)")
     ap.add_argument("--config", choices=CONFIG_NAMES, default=None,
                     help="with --configs: only this config (for a profiler run)")
+    ap.add_argument("--accuracy-grid", action="store_true",
+                    help="only the correct-bits table of the reference's accuracy study "
+                         "(six distributions x K 512/4096 at M = N = 128: native, default, "
+                         "reduced) and of its default-call depths, as JSON lines")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a float64 streaming kernel over 1 GiB (read 1 GiB, write "
                          "1 GiB) three times: the scale of the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
 
 
-CONFIG_NAMES = ("c1", "c2", "c3a", "c3b", "c4", "c5", "c5r")
+CONFIG_NAMES = ("c1", "c2", "c2i", "c2r", "c3a", "c3b", "c4", "c5", "c5r")
 
 
 def calibrate_copy():
@@ -81,6 +98,9 @@ def main():
     if args.calibrate_copy:
         calibrate_copy()
         return
+    if args.accuracy_grid:
+        accuracy_grid()
+        return
     if args.configs:
         run_configs(max(args.steps, 3), max(args.warmup, 1),
                     [args.config] if args.config else CONFIG_NAMES)
@@ -91,6 +111,7 @@ def main():
     from fp64_emu import capi
 
     dev = torch.device("cuda:0")
+    pin_rocblas()
     n = args.n
     M = N = K = n
     P, corr = fp64_emu.plan_config(K)
@@ -179,6 +200,19 @@ def main():
         cpu = cpu_baseline(A, Bt, P, corr)
         cpu_torch = cpu_torch_baseline(A, Bt)
 
+    configs = None
+    if not args.no_configs and n == 8192:
+        # Every other BASELINE config (and c2's other operating points) in
+        # the same run, timed through the torch op like the reference's
+        # benchmarks; the headline c2 line above is this table's c2 row.
+        del A, Bt, C
+        torch.cuda.empty_cache()
+        configs = run_configs(3, 1, [c for c in CONFIG_NAMES if c != "c2"], emit=False)
+        for r in configs:
+            log(f"config {r['config']}: {r['ms']:.3f} ms, {r['tflops']:.2f} TFLOP/s, "
+                f"{r['tflops'] / r['native_tflops']:.2f}x native, bits {r['correct_bits_emu']} / "
+                f"{r['correct_bits_native']}")
+
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "modgemm_c2_traffic.json")
     if n == 8192 and os.path.exists(tpath):
@@ -216,8 +250,47 @@ def main():
         **acc,
         "cpu_baseline": cpu,
         "cpu_torch_f64": cpu_torch,
+        "native_blas": native_blas(),
+        "configs": configs,
     }
     print(json.dumps(rec), flush=True)
+
+
+def accuracy_grid():
+    """Correct bits against the device double-double GEMM on the input
+    distributions of the reference's accuracy study (bench/accuracy.py:85-118,
+    README.md:200-213) and its default-call depths (bench/defaultcheck.py),
+    with inputs from the CPU seeds the GPU parity tests use."""
+    import torch
+    import fp64_emu
+    from fp64_emu import capi
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from distributions import DISTS, make, seed_of
+    dev = torch.device("cuda:0")
+
+    def bits(X, hi, lo):
+        err = ((X - hi) - lo).abs().max().item()
+        return 53.0 if err == 0 else round(-math.log2(err / hi.abs().max().item()), 2)
+
+    for dist in DISTS:
+        for K in (512, 4096):
+            A, Bt = make(dist, 128, K, 128, seed_of(dist, K))
+            A, Bt = A.to(dev), Bt.to(dev)
+            hi, lo = capi.ddgemm_nt(A, Bt.t().contiguous())
+            rec = {"table": "grid", "dist": dist, "K": K, "native": bits(A @ Bt, hi, lo),
+                   "default": bits(fp64_emu.mm_nt(A, Bt), hi, lo),
+                   "reduced": bits(fp64_emu.mm_nt(A, Bt, nprimes=13, corr=False), hi, lo)}
+            print(json.dumps(rec), flush=True)
+    for K in (64, 256, 1024, 4096):
+        for dist in ("randn", "wide16", "illcond40", "spike"):
+            A, Bt = make(dist, 128, K, 128, seed_of(dist, K) + 1)
+            A, Bt = A.to(dev), Bt.to(dev)
+            hi, lo = capi.ddgemm_nt(A, Bt.t().contiguous())
+            P, corr = fp64_emu.plan_config(K)
+            rec = {"table": "default_call", "dist": dist, "K": K, "plan": [P, corr],
+                   "native": bits(A @ Bt, hi, lo),
+                   "default": bits(fp64_emu.mm(A, Bt.t().contiguous()), hi, lo)}
+            print(json.dumps(rec), flush=True)
 
 
 def _config_inputs(name, torch):
@@ -227,9 +300,12 @@ def _config_inputs(name, torch):
     if name == "c1":
         return "mm_nt", torch.randn(128, 4096, dtype=torch.float64, generator=g(1000)), \
             torch.randn(4096, 128, dtype=torch.float64, generator=g(1001)), None
-    if name == "c2":
+    if name in ("c2", "c2i", "c2r"):
+        # c2i: the fp64 combine (exact=False, README.md:117-121); c2r: the
+        # reduced operating point, 13 moduli and no correction (README.md:137).
+        plan = {"c2": None, "c2i": (14, True, False), "c2r": (13, False)}[name]
         return "mm_nt", torch.randn(8192, 8192, dtype=torch.float64, generator=g(2000)), \
-            torch.randn(8192, 8192, dtype=torch.float64, generator=g(2001)), None
+            torch.randn(8192, 8192, dtype=torch.float64, generator=g(2001)), plan
     if name == "c3a":
         def wide(seed):
             gg = g(seed)
@@ -249,27 +325,30 @@ def _config_inputs(name, torch):
     return "mm_nt", A, B, ((13, False) if name == "c5r" else None)
 
 
-def run_configs(steps, warmup, names):
-    """One JSON line per BASELINE config: effective FP64 TFLOPS, the
+def run_configs(steps, warmup, names, emit=True):
+    """One record per BASELINE config: effective FP64 TFLOPS, the
     plan-adjusted INT8 roofline fraction, per-phase ms (mm_nt forms), the
     native float64 comparator and correct bits against the device
-    double-double GEMM."""
+    double-double GEMM.  Printed as JSON lines when `emit`; returned."""
     import torch
     import fp64_emu
     from fp64_emu import capi
     dev = torch.device("cuda:0")
+    pin_rocblas()
+    records = []
     for name in names:
         kind, A, B, plan = _config_inputs(name, torch)
         A, B = A.to(dev), B.to(dev)
         batched = kind == "bmm_nt"
         K = A.shape[-1]
-        P, corr = plan if plan else fp64_emu.plan_config(K)
+        P, corr = plan[:2] if plan else fp64_emu.plan_config(K)
+        exact = plan[2] if plan and len(plan) > 2 else True
         G = P + (2 if corr else 0)
         M, N = A.shape[-2], B.shape[-1]
         batch = A.shape[0] if batched else 1
         flop = 2.0 * batch * M * N * K
-        emu = (lambda: fp64_emu.bmm_nt(A, B, nprimes=P, corr=corr)) if batched else \
-            (lambda: fp64_emu.mm_nt(A, B, nprimes=P, corr=corr))
+        emu = (lambda: fp64_emu.bmm_nt(A, B, nprimes=P, corr=corr, exact=exact)) if batched else \
+            (lambda: fp64_emu.mm_nt(A, B, nprimes=P, corr=corr, exact=exact))
         nat = (lambda: torch.bmm(A, B)) if batched else (lambda: A @ B)
 
         def timed(fn):
@@ -300,7 +379,7 @@ def run_configs(steps, warmup, names):
             C = torch.empty(M, N, dtype=torch.float64, device=dev)
             evs = [capi.PhaseEvents() for _ in range(steps)]
             for i in range(steps):
-                capi.mm_nt_events(A, B, primes, C, ws, evs[i], use_corr=corr)
+                capi.mm_nt_events(A, B, primes, C, ws, evs[i], use_corr=corr, exact=exact)
             torch.cuda.synchronize()
             ph = [e.phases_ms() for e in evs]
             phases = [round(sum(p[i] for p in ph) / len(ph), 4) for i in range(4)]
@@ -321,44 +400,95 @@ def run_configs(steps, warmup, names):
             bits[tag] = 53.0 if errs == 0 else round(-math.log2(errs / scale), 2)
         value = flop / (ms * 1e-3) / 1e12
         rec = {"config": name, "kind": kind, "batch": batch, "M": M, "N": N, "K": K,
-               "nprimes": P, "corr": corr, "gemms": G, "ms": round(ms, 4),
+               "nprimes": P, "corr": corr, "exact": exact, "gemms": G, "ms": round(ms, 4),
                "tflops": round(value, 2),
                "plan_roofline_frac": round(value / (INT8_PEAK_TOPS / G), 4),
                "phases_ms": phases, "native_ms": round(nat_ms, 4),
                "native_tflops": round(flop / (nat_ms * 1e-3) / 1e12, 2),
                "correct_bits_emu": bits["emu"], "correct_bits_native": bits["native"]}
-        print(json.dumps(rec), flush=True)
+        if emit:
+            print(json.dumps(rec), flush=True)
+        records.append(rec)
         del A, B, Ce, Cn
         torch.cuda.empty_cache()
+    return records
 
 
 def _host_cores():
+    """The cores this process may use: its CPU affinity, capped at the 16
+    cores a one-GPU box of this pool allots to a GPU (OMP_NUM_THREADS there)."""
     try:
-        import psutil
-        cores = len(psutil.Process().cpu_affinity())
+        cores = len(os.sched_getaffinity(0))
     except Exception:
         cores = os.cpu_count() or 1
-    return max(1, min(cores, 16))
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return max(1, min(cores, cap) if cap > 0 else cores)
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def pin_rocblas():
+    """Route torch's device GEMMs through rocBLAS (torch's "cublas" backend on
+    ROCm) rather than hipBLASLt, for the native comparator."""
+    import torch
+    try:
+        torch.backends.cuda.preferred_blas_library("cublas")
+    except Exception as e:   # older torch: the environment variable set above
+        log(f"preferred_blas_library unavailable: {e}")
+
+
+def native_blas():
+    """Which library serves the native float64 comparator on the device."""
+    import torch
+    try:
+        pref = str(torch.backends.cuda.preferred_blas_library())
+    except Exception:
+        pref = "unknown"
+    return {"library": "rocBLAS (torch.matmul float64)", "torch_preferred_blas": pref,
+            "TORCH_BLAS_PREFER_HIPBLASLT": os.environ.get("TORCH_BLAS_PREFER_HIPBLASLT")}
 
 
 def cpu_torch_baseline(A, Bt):
     """torch float64 matmul of the same workload on the host's cores (the
-    comparison the reference's benchmarks quote beside native DGEMM)."""
+    comparison the reference's benchmarks quote beside native DGEMM): one
+    warm-up, then the median of three full products."""
+    import re
+    import statistics
     import torch
     cores = _host_cores()
     prev = torch.get_num_threads()
     torch.set_num_threads(cores)
     a, bt = A.cpu(), Bt.cpu()
-    torch.matmul(a[:1024], bt[:, :1024])            # warm-up
-    t0 = time.perf_counter()
-    torch.matmul(a, bt)
-    t = time.perf_counter() - t0
+    torch.matmul(a, bt)                               # warm-up
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        torch.matmul(a, bt)
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    used = torch.get_num_threads()
     torch.set_num_threads(prev)
+    cfg = torch.__config__.show()
+    blas = re.search(r"BLAS_INFO=([^,\n]+)", cfg)
     n = a.shape[0]
     val = 2.0 * n * bt.shape[1] * a.shape[1] / t / 1e12
-    log(f"cpu torch float64 matmul ({cores} threads): {t:.2f} s, {val:.4f} TFLOP/s")
-    return {"value": round(val, 5), "unit": "TFLOP/s", "cores": cores, "seconds": round(t, 3),
-            "sample": "the full workload, torch.matmul float64 on host tensors"}
+    log(f"cpu torch float64 matmul ({used} threads, {_cpu_model()}): median {t:.2f} s, "
+        f"{val:.4f} TFLOP/s")
+    return {"value": round(val, 5), "unit": "TFLOP/s", "cores": used, "seconds": round(t, 3),
+            "runs_s": [round(x, 3) for x in ts], "cpu_model": _cpu_model(),
+            "affinity_cores": len(os.sched_getaffinity(0)),
+            "blas": blas.group(1).strip() if blas else "unknown",
+            "sample": "the full workload, torch.matmul float64 on host tensors; median of 3 "
+                      "after 1 warm-up"}
 
 
 def cpu_baseline(A, Bt, P, corr):

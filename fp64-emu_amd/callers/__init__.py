@@ -1,4 +1,4 @@
-"""Callers of the emulated GEMM: the reference's tiled Cholesky
-(bench/cholesky.py) and application drills (bench/apps.py), written against
-this package.  Run as scripts for timings at the reference's sizes; the
+"""Callers of the emulated GEMM written against this package: a left-looking
+blocked Cholesky whose updates are batched products (blocked_cholesky.py) and
+application drills (drills.py).  Run as scripts for timings at full size; the
 GPU tests run them at reduced sizes with accuracy bars."""
