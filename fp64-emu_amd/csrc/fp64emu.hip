@@ -184,6 +184,27 @@ constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
+// Division of a work-group index (n < 2^31) by a launch constant d >= 1 with
+// one 32 x 32 high multiply, an add and a shift (Granlund and Montgomery,
+// "Division by invariant integers using multiplication", 1994, round-up
+// form): l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1, and
+// n / d = (mulhi(m, n) + n) >> l, exact for every n < 2^31 (the sum stays
+// below 2^32).  Work-group indices are uniform, so the divisions stay on the
+// scalar unit instead of the vector unit's float-reciprocal sequence.
+struct FastDiv {
+  uint32_t d, m, l;
+  __device__ __forceinline__ uint32_t div(uint32_t n) const { return (__umulhi(m, n) + n) >> l; }
+};
+
+FastDiv make_fastdiv(int64_t d) {
+  FastDiv f;
+  f.d = (uint32_t)std::max<int64_t>(d, 1);
+  f.l = 0;
+  while ((1ull << f.l) < f.d) ++f.l;
+  f.m = (uint32_t)(((1ull << 32) * ((1ull << f.l) - f.d)) / f.d + 1);
+  return f;
+}
+
 // Column-sizing slab split of a [K, N] operand; the same split as
 // fp64_emu_cuda/fp64_emu.cu:1159-1162 so the fp64 sum order matches.
 void slab_split(int64_t NF, int64_t K, int64_t* kslab, int* nslab) {
@@ -687,6 +708,9 @@ struct ExtractArgs {
   int64_t planeA, planeB, memberA, memberB;
   int64_t rgA, rgB;  // 64-row groups per member the GEMM reads (0: B not extracted)
   int64_t rgA_data, rgB_data;   // those holding operand rows: ceil(M / 64), ceil(N / 64)
+  // Dividers of the work-group decomposition: by nkt, and by the row-group
+  // count of each segment (A data, B data, A padding, B padding).
+  FastDiv div_nkt, div_rg[4];
   const int16_t* sftA;
   const int16_t* sftB;
   const int* bits_eff;
@@ -706,36 +730,40 @@ extract_kernel(ExtractArgs a) {
   // the all-padding row groups of A and of B (zero stores only), so that the
   // work spreads evenly over the XCDs (group i runs on XCD i % 8) whatever
   // the padding.
-  int64_t wg = blockIdx.x;
-  const int64_t nA = a.batch * a.rgA_data * a.nkt, nB = a.batch * a.rgB_data * a.nkt;
-  const int64_t nAp = a.batch * (a.rgA - a.rgA_data) * a.nkt;
+  uint32_t wg = blockIdx.x;
+  const uint32_t nA = (uint32_t)(a.batch * a.rgA_data * a.nkt), nB = (uint32_t)(a.batch * a.rgB_data * a.nkt);
+  const uint32_t nAp = (uint32_t)(a.batch * (a.rgA - a.rgA_data) * a.nkt);
   bool isA;
-  int64_t rg_per, rg_off = 0;
+  int seg;
+  int64_t rg_off = 0;
   if (wg < nA) {
-    isA = true; rg_per = a.rgA_data;
+    isA = true; seg = 0;
   } else if ((wg -= nA) < nB) {
-    isA = false; rg_per = a.rgB_data;
+    isA = false; seg = 1;
   } else if ((wg -= nB) < nAp) {
-    isA = true; rg_per = a.rgA - a.rgA_data; rg_off = a.rgA_data;
+    isA = true; seg = 2; rg_off = a.rgA_data;
   } else {
     wg -= nAp;
-    isA = false; rg_per = a.rgB - a.rgB_data; rg_off = a.rgB_data;
+    isA = false; seg = 3; rg_off = a.rgB_data;
   }
+  const FastDiv& rgd = a.div_rg[seg];
   const bool kn = !isA && a.b_kn;
   // Work group -> (member, 64-row group, k tile).  Row-major operands walk k
   // fastest (consecutive groups read consecutive bytes of the same rows);
   // the [K, N] operand walks the 64-column group fastest.
   int64_t b, rg, kt;
   if (kn) {
-    rg = wg % rg_per;
-    const int64_t t = wg / rg_per;
-    kt = t % a.nkt;
-    b = t / a.nkt;
+    const uint32_t t = rgd.div(wg);
+    rg = wg - t * rgd.d;
+    const uint32_t bb = a.div_nkt.div(t);
+    kt = t - bb * a.div_nkt.d;
+    b = bb;
   } else {
-    kt = wg % a.nkt;
-    const int64_t t = wg / a.nkt;
-    rg = t % rg_per;
-    b = t / rg_per;
+    const uint32_t t = a.div_nkt.div(wg);
+    kt = wg - t * a.div_nkt.d;
+    const uint32_t bb = rgd.div(t);
+    rg = t - bb * rgd.d;
+    b = bb;
   }
   rg += rg_off;
   const int64_t R = isA ? a.M : a.N;
@@ -1560,6 +1588,57 @@ modgemm_mixed_kernel(GemmArgs g) {
 
 typedef __int128 i128;
 
+// The default list's group products M0 = p_0 .. p_6 and M1 = p_7 .. p_13.
+constexpr long long default_group_product(int g) {
+  long long prod = 1;
+  for (int t = 7 * g; t < 7 * g + 7; ++t) prod *= kDefaultModuli[t];
+  return prod;
+}
+constexpr long long kDefaultM64[2] = {default_group_product(0), default_group_product(1)};
+
+// a m + c as a signed 128-bit (hi, lo) for |a| < 2^62, 0 <= m < 2^62 and
+// |c| < 2^61, with four signed 32 x 32 -> 64 multiply-adds: a = ah 2^32 + al
+// and m = mh 2^32 + ml with al, ml signed 32-bit, then
+//   q0 = al ml + c,  q1 = al mh + ah ml + (q0 >> 32),  q2 = ah mh + (q1 >> 32),
+// every partial below 2^63, and a m + c = (q0 mod 2^32) + (q1 mod 2^32) 2^32
+// + q2 2^64 (arithmetic shifts: floor division, so negative partials carry
+// correctly).
+__device__ __forceinline__ void mul_add_wide(int64_t a, uint64_t m, int64_t c, uint64_t& lo,
+                                             int64_t& hi) {
+  const int32_t al = (int32_t)(uint32_t)a;
+  const int32_t ah = (int32_t)(uint32_t)((uint64_t)a >> 32) + (int32_t)((uint32_t)a >> 31);
+  const int32_t ml = (int32_t)(uint32_t)m;
+  const int32_t mh = (int32_t)(uint32_t)(m >> 32) + (int32_t)((uint32_t)m >> 31);
+  const int64_t q0 = (int64_t)al * ml + c;
+  const int64_t q1 = (int64_t)al * mh + (int64_t)ah * ml + (q0 >> 32);
+  const int64_t q2 = (int64_t)ah * mh + (q1 >> 32);
+  lo = ((uint64_t)(uint32_t)q1 << 32) | (uint32_t)q0;
+  hi = q2;
+}
+
+// Loads and stores through a base address the caller knows to be uniform
+// across the wave (moved to scalar registers) plus a 32-bit per-lane byte
+// offset: the global scalar-base form, instead of a 64-bit vector address
+// per access.
+typedef __attribute__((address_space(1))) char gchar;
+
+__device__ __forceinline__ gchar* uniform_base(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<gchar*>(((uint64_t)hi << 32) | lo);
+}
+
+template <typename T>
+__device__ __forceinline__ T load_at(const void* base, uint32_t byte_off) {
+  return *reinterpret_cast<const __attribute__((address_space(1))) T*>(uniform_base(base) + byte_off);
+}
+
+template <typename T>
+__device__ __forceinline__ void store_at(void* base, uint32_t byte_off, T v) {
+  *reinterpret_cast<__attribute__((address_space(1))) T*>(uniform_base(base) + byte_off) = v;
+}
+
 // Exactly rounded (to nearest, ties to even) double of a signed 64-bit integer:
 // the high word scaled by 2^32 is exact, the one fma rounds the sum once.
 __device__ __forceinline__ double i64_to_f64(int64_t v) {
@@ -1597,6 +1676,8 @@ struct ReconArgs {
   int64_t NB;          // 64-column blocks per padded output row (Np / 64)
   int64_t MBv, NBv;    // 16-row and 64-column blocks covering the valid M, N
   int64_t nblocks;     // batch * MBv * NBv
+  FastDiv per_div;     // by MBv * NBv (blocks per member)
+  FastDiv nbv_div;     // by NBv
   int ncorr;
   int ksplit;            // S: residue / correction planes per output, summed here
   ModTables tab;
@@ -1611,29 +1692,41 @@ struct ReconArgs {
 template <bool kExact, bool kDeep, int kP, bool kSplit>
 __global__ void __launch_bounds__(kThreads)
 reconstruct_kernel(ReconArgs a) {
-  const int64_t blk = blockIdx.x;
-  if (blk >= a.nblocks) return;
+  // Block -> (member, 16-row block, 64-column block): uniform, so every
+  // address below is a scalar base plus a 32-bit per-lane offset.
+  const uint32_t blk = blockIdx.x;
+  const uint32_t b = a.per_div.div(blk);
+  const uint32_t rem = blk - b * a.per_div.d;
+  const uint32_t mb = a.nbv_div.div(rem);
+  const uint32_t nb = rem - mb * a.nbv_div.d;
   const int thr = threadIdx.x;
-  const int64_t per = a.MBv * a.NBv;
-  const int64_t b = blk / per;
-  const int64_t rem = blk - b * per;
-  const int64_t mb = rem / a.NBv, nb = rem - (rem / a.NBv) * a.NBv;
   const int l = thr >> 2, q4 = thr & 3;
-  const int64_t i0 = mb * 16 + 4 * (l >> 4);
-  const int64_t j = nb * 64 + 16 * q4 + (l & 15);
-  if (j >= a.N || i0 >= a.M) return;
+  // This thread's first row in the block: 4 per wave, so uniform per wave
+  // (scalar row checks, shift loads and store bases).
+  const int row0 = 4 * __builtin_amdgcn_readfirstlane(thr >> 6);
+  const int col = 16 * q4 + (l & 15);          // its column in the block
+  const int64_t j = (int64_t)nb * 64 + col;
+  const int64_t rows_left = a.M - (int64_t)mb * 16;   // valid rows from the block's first
+  if (j >= a.N || row0 >= rows_left) return;
 
   const int P = kP > 0 ? kP : a.tab.P;
   constexpr bool kUsual = kP > 0;
-  const int64_t boff = (mb * a.NB + nb) * 1024 + 4 * thr;  // byte (int8) / element (int32)
+  // Byte (int8 planes) / element (int32 planes) offset of this block, and
+  // the lane's offset inside it.
+  const int64_t boff0 = ((int64_t)mb * a.NB + nb) * 1024;
+  const uint32_t lane4 = 4u * (uint32_t)thr;
+  const int64_t boff = boff0 + lane4;
   // The output scalings, read with the residues (one round trip, instead of
   // a dependent load per element at the end); rows past M read row M - 1.
   // Both shifts grew by bits_eff[1] at the width pick.
   const int cshift = a.bits_eff[0] - 15;
-  const int sj = (int)a.sftB[b * a.N + j] + 2 * a.bits_eff[1];
+  const int16_t* sftB_blk = a.sftB + (int64_t)b * a.N + (int64_t)nb * 64;
+  const int sj = (int)load_at<int16_t>(sftB_blk, 2u * col) + 2 * a.bits_eff[1];
+  const int16_t* sftA_blk = a.sftA + (int64_t)b * a.M + (int64_t)mb * 16;
+  const int last_row = (int)(rows_left < 16 ? rows_left : 16) - 1;
   int sai[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) sai[e] = (int)a.sftA[b * a.M + min(i0 + e, a.M - 1)];
+  for (int e = 0; e < 4; ++e) sai[e] = (int)load_at<int16_t>(sftA_blk, 2u * min(row0 + e, last_row));
   uint32_t w[kMaxP];
   int64_t cv[4] = {0, 0, 0, 0};
   if (kDeep) {
@@ -1653,9 +1746,10 @@ reconstruct_kernel(ReconArgs a) {
       for (int e = 0; e < 4; ++e) cv[e] = c[e];
     }
   } else if (!kSplit) {
+    const int8_t* rb = a.res8 + (int64_t)b * P * a.outplane + boff0;
 #pragma unroll
     for (int t = 0; t < kMaxP; ++t)
-      if (t < P) w[t] = *reinterpret_cast<const uint32_t*>(a.res8 + (b * P + t) * a.outplane + boff);
+      if (t < P) w[t] = load_at<uint32_t>(rb + t * a.outplane, lane4);
   } else {
     // K-split: the S partial residues sum (|sum| <= 128 S) and fold to the
     // residue (any representative serves: each digit reduces mod p again),
@@ -1714,11 +1808,12 @@ reconstruct_kernel(ReconArgs a) {
       }
   }
   if (!kDeep && !kSplit && a.ncorr > 0) {   // (a K-split summed them above)
-    const v4i c1 = *reinterpret_cast<const v4i*>(a.corr + (b * a.ncorr) * a.outplane + boff);
+    const int32_t* cb = a.corr + (int64_t)b * a.ncorr * a.outplane + boff0;
+    const v4i c1 = load_at<v4i>(cb, 4 * lane4);
 #pragma unroll
     for (int e = 0; e < 4; ++e) cv[e] = c1[e];
     if (a.ncorr == 2) {
-      const v4i c2 = *reinterpret_cast<const v4i*>(a.corr + (b * a.ncorr + 1) * a.outplane + boff);
+      const v4i c2 = load_at<v4i>(cb + a.outplane, 4 * lane4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) cv[e] += c2[e];
     }
@@ -1790,7 +1885,10 @@ reconstruct_kernel(ReconArgs a) {
     }
   }
 
-  double* outp = a.out + (b * a.M + i0) * a.N + j;
+  // The wave's output rows from a uniform base; the lane's byte offset is
+  // its column's.
+  double* const oblk = a.out + ((int64_t)b * a.M + (int64_t)mb * 16 + row0) * a.N + (int64_t)nb * 64;
+  const uint32_t olane = 8u * (uint32_t)col;
 
   // Horner per group of 7 (digits 7g .. 7g+6, high to low), in two int32
   // halves: positions 6..3 give H (four balanced digits stay below 2^31;
@@ -1826,25 +1924,43 @@ reconstruct_kernel(ReconArgs a) {
   const int ng = (P + 6) / 7;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const int64_t i = i0 + e;
-    if (i >= a.M) continue;
+    if (row0 + e >= rows_left) continue;
     // Every group ends on its position-0 digit, an int64 step, so ag holds
     // the group value whatever the group's digit count.
     const long long a0 = ag[e][0], a1 = ag[e][1], a2 = ag[e][2];
     const int sh = -(sai[e] + sj);
     double val;
     if (kExact) {
-      i128 acc = ng == 3 ? (i128)a2 : (ng == 2 ? (i128)a1 : (i128)a0);
-      if (ng == 3) acc = acc * (i128)(uint64_t)a.tab.m64[1] + a1;
-      if (ng >= 2) acc = acc * (i128)(uint64_t)a.tab.m64[0] + a0;
+      // X = a0 + M0 (a1 + M1 a2) as a 128-bit word pair (hi, lo).  The one
+      // or two group products of the usual plans (at most 15 moduli: group 2
+      // holds at most one digit, so a1 + M1 a2 fits 63 bits) take
+      // mul_add_wide's four 32 x 32 -> 64 multiply-adds; longer lists take
+      // the general 128-bit product (the true X stays below 2^127, so the
+      // products wrap modulo 2^128 harmlessly).
+      const uint64_t m0 = kUsual ? (uint64_t)kDefaultM64[0] : (uint64_t)a.tab.m64[0];
+      const uint64_t m1 = kUsual ? (uint64_t)kDefaultM64[1] : (uint64_t)a.tab.m64[1];
+      uint64_t lo;
+      int64_t hi;
+      if (ng == 1) {
+        lo = (uint64_t)a0;
+        hi = a0 >> 63;
+      } else if (ng == 2 || (kUsual && P == 15)) {
+        const int64_t top = ng == 2 ? a1 : (int64_t)((uint64_t)a2 * m1) + a1;
+        mul_add_wide(top, m0, a0, lo, hi);
+      } else {
+        i128 acc = (i128)a2 * (i128)m1 + a1;
+        acc = acc * (i128)m0 + a0;
+        lo = (uint64_t)acc;
+        hi = (int64_t)(acc >> 64);
+      }
       // + corr 2^cshift: 1 <= cshift <= 38 (bits_eff in [16, 53]), so the
       // shifted value is the word pair (cv >> (64 - cshift), cv << cshift).
       const unsigned __int128 cw =
           ((unsigned __int128)(uint64_t)(cv[e] >> (64 - cshift)) << 64) | ((uint64_t)cv[e] << cshift);
-      acc = (i128)((unsigned __int128)acc + cw);
-      const unsigned __int128 u = (unsigned __int128)acc;
-      outp[e * a.N] = i128w_to_f64((uint32_t)u, (uint32_t)(u >> 32), (uint32_t)(u >> 64),
-                                   (uint32_t)(u >> 96), sh);
+      const unsigned __int128 u = (((unsigned __int128)(uint64_t)hi << 64) | lo) + cw;
+      store_at<double>(oblk + e * a.N, olane,
+                       i128w_to_f64((uint32_t)u, (uint32_t)(u >> 32), (uint32_t)(u >> 64),
+                                    (uint32_t)(u >> 96), sh));
       continue;
     } else {
       double acc = (double)(ng == 3 ? a2 : (ng == 2 ? a1 : a0));
@@ -1853,7 +1969,7 @@ reconstruct_kernel(ReconArgs a) {
       acc = acc + ldexp((double)cv[e], cshift);
       val = acc;
     }
-    outp[e * a.N] = ldexp(val, sh);
+    store_at<double>(oblk + e * a.N, olane, ldexp(val, sh));
   }
 }
 
@@ -2160,6 +2276,11 @@ int run(const Call& c) {
       ea.memberA = L.memberA_bytes; ea.memberB = L.memberB_bytes;
       ea.rgA = L.ext_rowsA / 64; ea.rgB = with_B ? L.ext_rowsB / 64 : 0;
       ea.rgA_data = (Mc + 63) / 64; ea.rgB_data = with_B ? (c.N + 63) / 64 : 0;
+      ea.div_nkt = make_fastdiv(nkt);
+      ea.div_rg[0] = make_fastdiv(ea.rgA_data);
+      ea.div_rg[1] = make_fastdiv(ea.rgB_data);
+      ea.div_rg[2] = make_fastdiv(ea.rgA - ea.rgA_data);
+      ea.div_rg[3] = make_fastdiv(ea.rgB - ea.rgB_data);
       ea.sftA = sftA + m0; ea.sftB = sftB; ea.bits_eff = bits_eff;
       ea.planesA = planesA; ea.planesB = planesB;
       ea.tab = tab;
@@ -2213,6 +2334,8 @@ int run(const Call& c) {
     ra.NB = L.Np / 64;
     ra.MBv = (Mc + 15) / 16; ra.NBv = (c.N + 63) / 64;
     ra.nblocks = c.batch * ra.MBv * ra.NBv;
+    ra.per_div = make_fastdiv(ra.MBv * ra.NBv);
+    ra.nbv_div = make_fastdiv(ra.NBv);
     ra.ncorr = L.ncorr;
     ra.ksplit = L.ksplit;
     ra.tab = tab;
