@@ -512,20 +512,23 @@ __device__ __forceinline__ void size_cols_partial_body(int64_t bx, int64_t by, c
 }
 
 // The sizing of A's rows and of the [K, N] operand's column slabs in one
-// launch: groups [0, nrow) size rows, the rest column slabs (x fastest).
+// launch: groups [0, ncol) take column slabs (x fastest), the rest rows.
+// The slab groups come first: each thread walks its slab's rows in one
+// dependent chain, so they are the launch's longest groups, and starting
+// them first lets the row groups fill in around them instead of leaving
+// them as a tail.
 template <bool kGroup>
 __global__ void __launch_bounds__(kThreads)
-size_rows_cols_kernel(const double* __restrict__ A, int64_t rowsA, int64_t nrow, int64_t K, int bits,
+size_rows_cols_kernel(const double* __restrict__ A, int64_t rowsA, int64_t ncol, int64_t K, int bits,
                       int16_t* __restrict__ sftA, float* __restrict__ lgA,
                       const double* __restrict__ X, int64_t totalcols, int64_t cols_per,
                       int64_t kslab, int64_t gcx, double* __restrict__ pmax,
                       double* __restrict__ pss) {
   const int64_t bid = blockIdx.x;
-  if (bid < nrow) {
-    size_rows_body<kGroup>(bid, A, rowsA, A, rowsA, K, bits, sftA, lgA, nullptr, nullptr);
+  if (bid < ncol) {
+    size_cols_partial_body(bid % gcx, bid / gcx, X, totalcols, K, cols_per, kslab, pmax, pss);
   } else {
-    const int64_t q = bid - nrow;
-    size_cols_partial_body(q % gcx, q / gcx, X, totalcols, K, cols_per, kslab, pmax, pss);
+    size_rows_body<kGroup>(bid - ncol, A, rowsA, A, rowsA, K, bits, sftA, lgA, nullptr, nullptr);
   }
 }
 
@@ -2241,11 +2244,12 @@ int run(const Call& c) {
     const bool group = MF < kRowsGroupBelow;
     const int64_t nrow = group ? MF : (MF + kRowsPerBlock - 1) / kRowsPerBlock;
     const unsigned grid = (unsigned)(nrow + gcx * nslab);
+    const int64_t ncol = gcx * nslab;
     if (group)
-      hipLaunchKernelGGL(size_rows_cols_kernel<true>, dim3(grid), dim3(kThreads), 0, s, c.A, MF, nrow,
+      hipLaunchKernelGGL(size_rows_cols_kernel<true>, dim3(grid), dim3(kThreads), 0, s, c.A, MF, ncol,
                          c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, gcx, pmax, pss);
     else
-      hipLaunchKernelGGL(size_rows_cols_kernel<false>, dim3(grid), dim3(kThreads), 0, s, c.A, MF, nrow,
+      hipLaunchKernelGGL(size_rows_cols_kernel<false>, dim3(grid), dim3(kThreads), 0, s, c.A, MF, ncol,
                          c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, gcx, pmax, pss);
     hipLaunchKernelGGL(size_cols_final_kernel, dim3((unsigned)((NF + kFinalCols - 1) / kFinalCols)),
                        dim3(kThreads), 0, s, pmax, pss, NF, nslab, c.bits, sftB, lgB);
