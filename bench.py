@@ -17,7 +17,7 @@ against a device double-double GEMM, the plan-adjusted INT8 roofline
 fraction, the `roofline` object for the dominant kernel (the modular GEMM,
 its duration from the events bracketing its launch in every timed call), the CPU
 baseline (the oracle port on a bounded sample of the same workload), torch
-float64 matmul on the host's cores, and under "configs" every other BASELINE
+float64 matmul on the host's cores, and under "configs" every other benchmark
 config (c1, c3a, c3b, c4, c5, c5 reduced) plus c2 with the fp64 combine (c2i)
 and at the reduced plan (c2r), each with its ms, TFLOP/s, plan fraction,
 phases, native comparator and correct bits.
@@ -54,7 +54,7 @@ def parse():
                          "c3b, c4, c5, c5 reduced) that the headline line carries under "
                          "\"configs\"")
     ap.add_argument("--configs", action="store_true",
-                    help="instead of the headline line, one JSON line per BASELINE config "
+                    help="instead of the headline line, one JSON line per benchmark config "
                          "(c1, c2, c3a, c3b, c4, c5 default and reduced)")
     ap.add_argument("--config", choices=CONFIG_NAMES, default=None,
                     help="with --configs: only this config (for a profiler run)")
@@ -202,7 +202,7 @@ def main():
 
     configs = None
     if not args.no_configs and n == 8192:
-        # Every other BASELINE config (and c2's other operating points) in
+        # Every other benchmark config (and c2's other operating points) in
         # the same run, timed through the torch op like the reference's
         # benchmarks; the headline c2 line above is this table's c2 row.
         del A, Bt, C
@@ -294,7 +294,7 @@ def accuracy_grid():
 
 
 def _config_inputs(name, torch):
-    """Inputs of the BASELINE configs, generated on the CPU (seeds 1000 cfg,
+    """Inputs of the benchmark configs c1 .. c5, generated on the CPU (seeds 1000 cfg,
     1000 cfg + 1)."""
     g = lambda seed: torch.Generator().manual_seed(seed)  # noqa: E731
     if name == "c1":
@@ -326,7 +326,7 @@ def _config_inputs(name, torch):
 
 
 def run_configs(steps, warmup, names, emit=True):
-    """One record per BASELINE config: effective FP64 TFLOPS, the
+    """One record per benchmark config: effective FP64 TFLOPS, the
     plan-adjusted INT8 roofline fraction, per-phase ms (mm_nt forms), the
     native float64 comparator and correct bits against the device
     double-double GEMM.  Printed as JSON lines when `emit`; returned."""
