@@ -1,9 +1,11 @@
-"""GPU parity over a seeded sweep of small shapes: every stage of the HIP
+"""GPU parity over seeded sweeps of small shapes: every stage of the HIP
 path against the CPU oracle (through the C ABI, on a pattern-filled
 workspace), for kinds, batch counts, ragged M / N / K, modulus counts,
 correction on and off and both combines drawn from a fixed generator.  The
 draws reach every GEMM launch form (256 x 256, 256 x 128, 128 x 128 and
-mixed tiles; K-splits; slot runs), as a CPU-tier test of the draws checks."""
+mixed tiles; K-splits; slot runs), as a CPU-tier test of the draws checks.
+A second sweep draws the reference accuracy study's input distributions
+(wide exponent ranges, ill-conditioned scalings, spikes) at ragged shapes."""
 import numpy as np
 import pytest
 import torch
@@ -47,3 +49,31 @@ def test_sweep_parity(dev, i, kind, batch, M, N, K, P, corr, exact):
         B = torch.randn((K, N) if kind == "mm_nt" else (N, K), dtype=torch.float64, generator=g)
     check_call(kind, A.to(dev), B.to(dev), O.PRIMES[:P], exact=exact, use_corr=corr)
 
+
+
+def _dist_cases():
+    """Seeded draws over the reference accuracy study's input distributions
+    (tests/distributions.py) at ragged shapes, modulus counts and plans."""
+    from distributions import DISTS
+    rng = np.random.default_rng(20261203)
+    out = []
+    for i in range(18):
+        dist = DISTS[i % len(DISTS)]
+        kind = ["mm", "mm_nt"][rng.integers(2)]
+        M = int(rng.integers(1, 500))
+        N = int(rng.integers(1, 700))
+        K = int(rng.integers(1, 6000))
+        P = int(rng.integers(12, 21))
+        corr = bool(rng.integers(4))           # mostly with the correction
+        exact = bool(rng.integers(4))
+        out.append((i, dist, kind, M, N, K, P, corr, exact))
+    return out
+
+
+@pytest.mark.parametrize("i,dist,kind,M,N,K,P,corr,exact", _dist_cases())
+def test_sweep_distributions(dev, i, dist, kind, M, N, K, P, corr, exact):
+    from distributions import make
+    print(f"case dist-sweep {i}: {dist} {kind} {M}x{N}x{K} P={P} corr={corr} exact={exact}", flush=True)
+    A, Bt = make(dist, M, K, N, 9000 + i)
+    B = Bt if kind == "mm_nt" else Bt.t().contiguous()
+    check_call(kind, A.to(dev), B.to(dev), O.PRIMES[:P], exact=exact, use_corr=corr)
