@@ -99,9 +99,12 @@ struct GarnerTab {
   // Balanced int8 factors of digit t, 4 per word: byte u < t holds
   // -M_u minv_t mod p_t.
   int nmp[kMaxP * kGarnerWords];
+  // The same factors as unsigned bytes in [0, p_t), for digits in [0, p).
+  uint32_t ump[kMaxP * kGarnerWords];
   int mib[kMaxP];                  // minv_t = (M_t mod p_t)^-1 mod p_t, M_t = prod_{u<t} p_u,
                                    // balanced (an int8)
   double invp[kMaxP];              // RN(1 / p)
+  uint32_t mq[kMaxP];              // ceil(2^32 / p): floor(y / p) = mulhi(y, mq) for y < 2^20
   int c31[kMaxP];                  // 2^31 mod p, balanced (the extraction's limb factor)
 };
 
@@ -118,6 +121,7 @@ __host__ __device__ constexpr GarnerTab garner_tables(const int* primes, int P) 
       int bal = (int)v;
       if (bal > (pt - 1) / 2) bal -= pt;
       T.nmp[t * kGarnerWords + (u >> 2)] |= (int)((uint32_t)(uint8_t)(int8_t)bal << (8 * (u & 3)));
+      T.ump[t * kGarnerWords + (u >> 2)] |= (uint32_t)v << (8 * (u & 3));
     };
     long long Mu = 1 % pt;         // M_u mod p_t, running over u
     for (int u = 0; u < t; ++u) {
@@ -125,6 +129,7 @@ __host__ __device__ constexpr GarnerTab garner_tables(const int* primes, int P) 
       Mu = (Mu * (primes[u] % pt)) % pt;
     }
     T.mib[t] = 2 * mi > pt ? mi - pt : mi;
+    T.mq[t] = (uint32_t)(((1ULL << 32) + (unsigned long long)pt - 1) / (unsigned long long)pt);
     const int c31 = (int)((1LL << 31) % pt);
     T.c31[t] = 2 * c31 > pt ? c31 - pt : c31;
   }
@@ -137,6 +142,21 @@ __host__ __device__ constexpr GarnerTab garner_tables(const int* primes, int P) 
 constexpr int kDefaultModuli[kMaxP] = {256, 255, 253, 251, 247, 241, 239, 233, 229, 227,
                                        223, 217, 211, 199, 197, 193, 191, 181, 179, 173};
 __device__ constexpr GarnerTab kDefaultTab = garner_tables(kDefaultModuli, kMaxP);
+// The default-list reconstruction computes the mixed-radix digits of
+// X + M/2 (in [0, p_t)) instead of X's balanced ones: since every default
+// modulus is 256 or odd, M/2 = sum_t (p_t >> 1) W_t, so digit t of X + M/2 is
+// X's balanced digit plus p_t >> 1, and X + M/2 has X's residues except
+// r_0 + 128 for p_0 = 256 (M/2 is a multiple of every odd p_t).  Group g's
+// balanced value (digits 7g .. 7g+6 at their weights inside the group) is
+// then the unsigned one minus this offset.
+constexpr long long default_digit_offset(int P, int g) {
+  long long off = 0, w = 1;
+  for (int t = 7 * g; t < 7 * g + 7 && t < P; ++t) {
+    off += (long long)(kDefaultModuli[t] >> 1) * w;
+    w *= kDefaultModuli[t];
+  }
+  return off;
+}
 // The extraction's default-list kernel takes the 24-bit residue path for
 // every plane without a tie fix: each default modulus is 256 or odd, and >= 171.
 constexpr bool default_moduli_plain() {
@@ -1673,6 +1693,35 @@ __device__ __forceinline__ double i128w_to_f64(uint32_t w0, uint32_t w1, uint32_
   return ldexp(i64_to_f64((int64_t)top), 64 - k + sh);
 }
 
+// The same rounding without a branch between long and short values.  k =
+// the value's redundant sign bits, capped at 64: the leading zeros of
+// V = ((hi ^ s) << 1) | ((lo ^ s) >> 63), s the sign word (V = 0 when the
+// value fits in 64 bits).  Shifted left by k, the value's top 64 bits hold 63
+// significant bits (k < 64) or all of it (k = 64: lo, whose top bit is the
+// sign, so hi << 63 ORs nothing new in); the dropped tail (the low 64 - k bits
+// of lo; for k = 64 lo's bit 0, already the result's bit 0) ORs into the
+// lowest bit.  A magnitude of 2^126 or more (k = 0, beyond every plan's
+// range) takes the general form above.  sh64 = sh + 64.
+__device__ __forceinline__ double i128_to_f64(int64_t hi, uint64_t lo, int sh64) {
+  const uint32_t s = (uint32_t)(int32_t)(hi >> 63);
+  const uint32_t th = (uint32_t)((uint64_t)hi >> 32) ^ s, tl = (uint32_t)hi ^ s;
+  const uint32_t u = (uint32_t)(lo >> 32) ^ s;
+  const uint64_t V = ((uint64_t)__builtin_amdgcn_alignbit(th, tl, 31) << 32) |
+                     __builtin_amdgcn_alignbit(tl, u, 31);
+  const int k = V == 0 ? 64 : __builtin_clzll(V);
+  if (k == 0)
+    return i128w_to_f64((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi,
+                        (uint32_t)((uint64_t)hi >> 32), sh64 - 64);
+  const int kk = k < 63 ? k : 63;
+  const uint64_t dropped = lo << kk;
+  // min(tail, 1) as one instruction (the compiler's compare-and-select form
+  // takes two).
+  uint32_t sticky;
+  asm("v_min_u32 %0, 1, %1" : "=v"(sticky) : "v"((uint32_t)dropped | (uint32_t)(dropped >> 32)));
+  const uint64_t top = ((uint64_t)hi << kk) | (lo >> (64 - k)) | sticky;
+  return ldexp(i64_to_f64((int64_t)top), sh64 - k);
+}
+
 struct ReconArgs {
   const int8_t* res8;
   const int32_t* corr;
@@ -1844,54 +1893,103 @@ reconstruct_kernel(ReconArgs a) {
   for (int e = 0; e < 4; ++e)
 #pragma unroll
     for (int g = 0; g < kGarnerWords; ++g) dp[e][g] = 0;
-#pragma unroll
-  for (int t = 0; t < kMaxP; ++t) {
-    if (t >= P) continue;
-    const int pt = tab_p(t);
-    if (t == 0) {
-      // M_0 = 1: the first digit is the residue.  The GEMM epilogue and the
-      // folds above leave it in [-p/2, (p-1)/2] for odd p (nearest quotient)
-      // and for p = 256 (any representative's low byte is that range); any
-      // other even p is brought there by the floor rule of barrett_bal32.
-      const bool norm = !kUsual && !(pt & 1) && pt != 256;
-      const double pd0 = (double)pt, ip0 = tab_invp(0);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        int d = (int)(int8_t)(uint8_t)(w[0] >> (8 * e));
-        if (norm) {
-          const double rd = (double)d;
-          d = (int)fma(-floor(fma(rd, ip0, kHalfUp)), pd0, rd);
-        }
-        dg[e][0] = d;
-        dp[e][0] = d;   // bytes 1..3 meet zero factors until digits 1..3 land there
-      }
-      continue;
-    }
-    const double nip = -tab_invp(t);
-    int nmw[kGarnerWords];
-#pragma unroll
-    for (int g = 0; g < kGarnerWords; ++g) nmw[g] = (4 * g < t) ? tab_nmp(t * kGarnerWords + g) : 0;
-    const int mib = tab_mib(t);
-    const int sh = 8 * (t & 3);
+  if constexpr (kUsual) {
+    // The digits of X + M/2, in [0, p_t) (default_digit_offset): digit 0 is
+    // r_0 + 128, the residue byte with its top bit flipped; digit t is y mod
+    // p_t for y = 128 p_t + r_t minv_t + sum_{u<t} d_u (-M_u minv_t mod p_t),
+    // the sum as unsigned dot products of digit bytes and factor bytes in
+    // [0, p_t), so 0 < y < 2^21 and its quotient by p_t is one high multiply
+    // (mq = ceil(2^32 / p_t): exact below 2^24).
+    const uint32_t u0 = w[0] ^ 0x80808080u;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      // y = (r_t - sum_{u<t} d_u M_u) minv_t mod p_t as dot products: r_t
-      // minv_t from byte e of the residue word (the factor word holds minv_t
-      // at byte e only), then the digits' terms; |y| < 20 * 2^14.
-      int y = sdot4_zero(w[t], (uint32_t)(uint8_t)(int8_t)mib << (8 * e));
+      const uint32_t s0 = u0 >> (8 * e);
+      dg[e][0] = (int)(s0 & 0xFFu);
+      dp[e][0] = (int)s0;   // bytes 1..3 meet zero factors until digits 1..3 land there
+    }
 #pragma unroll
-      for (int g = 0; g < kGarnerWords; ++g)
-        if (4 * g < t) y = __builtin_amdgcn_sdot4(dp[e][g], nmw[g], y, false);
-      // d = y - p q, q the nearest integer to y/p (-q is the low word of the
-      // fma rounding -y/p; |q| < 2^19).  Odd p has no ties: d lies in
-      // [-(p-1)/2, (p-1)/2].  Even p may give +p/2, barrett_bal32's -p/2.
-      int d = __mul24(__double2loint(fma((double)y, nip, kMagic)), pt) + y;
-      if (!kUsual && !(pt & 1)) d = d == (pt >> 1) ? -(pt >> 1) : d;
-      dg[e][t] = d;
-      // Insert the digit's low byte at byte t % 4 of its word.
-      dp[e][t >> 2] = (t & 3) == 0 ? d
-                                   : (int)__builtin_amdgcn_perm((uint32_t)d, (uint32_t)dp[e][t >> 2],
-                                                                 (0x03020100u & ~(0xFFu << sh)) | (0x04u << sh));
+    for (int t = 1; t < kMaxP; ++t) {
+      if (t >= P) continue;
+      const int pt = kDefaultModuli[t];
+      const int mib = kDefaultTab.mib[t];
+      const uint32_t mq = kDefaultTab.mq[t];
+      const int sh = 8 * (t & 3);
+      // 128 p_t in one register for the four elements' first dot products
+      // (kept opaque: the compiler would otherwise rematerialise it into each
+      // chain's accumulator, one move per element).
+      uint32_t bias;
+      asm volatile("v_mov_b32 %0, %1" : "=v"(bias) : "i"(128 * pt));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // The digits' terms first (from 128 p_t), then r_t minv_t from byte e
+        // of the residue word (the factor word holds minv_t at byte e only).
+        // (Issuing the residue term first, off the digit-to-digit chain, in
+        // the three-operand form with the factor in a scalar register
+        // measured 3% slower at 8192^3.)
+        uint32_t y = bias;
+#pragma unroll
+        for (int g = 0; g < kGarnerWords; ++g)
+          if (4 * g < t)
+            y = __builtin_amdgcn_udot4((uint32_t)dp[e][g], kDefaultTab.ump[t * kGarnerWords + g], y, false);
+        y = (uint32_t)__builtin_amdgcn_sdot4((int)w[t], (int)((uint32_t)(uint8_t)(int8_t)mib << (8 * e)),
+                                             (int)y, false);
+        const int d = __mul24((int)__umulhi(y, mq), -pt) + (int)y;
+        dg[e][t] = d;
+        dp[e][t >> 2] = (t & 3) == 0 ? d
+                                     : (int)__builtin_amdgcn_perm((uint32_t)d, (uint32_t)dp[e][t >> 2],
+                                                                   (0x03020100u & ~(0xFFu << sh)) | (0x04u << sh));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < kMaxP; ++t) {
+      if (t >= P) continue;
+      const int pt = tab_p(t);
+      if (t == 0) {
+        // M_0 = 1: the first digit is the residue.  The GEMM epilogue and the
+        // folds above leave it in [-p/2, (p-1)/2] for odd p (nearest quotient)
+        // and for p = 256 (any representative's low byte is that range); any
+        // other even p is brought there by the floor rule of barrett_bal32.
+        const bool norm = !(pt & 1) && pt != 256;
+        const double pd0 = (double)pt, ip0 = tab_invp(0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          int d = (int)(int8_t)(uint8_t)(w[0] >> (8 * e));
+          if (norm) {
+            const double rd = (double)d;
+            d = (int)fma(-floor(fma(rd, ip0, kHalfUp)), pd0, rd);
+          }
+          dg[e][0] = d;
+          dp[e][0] = d;   // bytes 1..3 meet zero factors until digits 1..3 land there
+        }
+        continue;
+      }
+      const double nip = -tab_invp(t);
+      int nmw[kGarnerWords];
+#pragma unroll
+      for (int g = 0; g < kGarnerWords; ++g) nmw[g] = (4 * g < t) ? tab_nmp(t * kGarnerWords + g) : 0;
+      const int mib = tab_mib(t);
+      const int sh = 8 * (t & 3);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // y = (r_t - sum_{u<t} d_u M_u) minv_t mod p_t as dot products: r_t
+        // minv_t from byte e of the residue word (the factor word holds minv_t
+        // at byte e only), then the digits' terms; |y| < 20 * 2^14.
+        int y = sdot4_zero(w[t], (uint32_t)(uint8_t)(int8_t)mib << (8 * e));
+#pragma unroll
+        for (int g = 0; g < kGarnerWords; ++g)
+          if (4 * g < t) y = __builtin_amdgcn_sdot4(dp[e][g], nmw[g], y, false);
+        // d = y - p q, q the nearest integer to y/p (-q is the low word of the
+        // fma rounding -y/p; |q| < 2^19).  Odd p has no ties: d lies in
+        // [-(p-1)/2, (p-1)/2].  Even p may give +p/2, barrett_bal32's -p/2.
+        int d = __mul24(__double2loint(fma((double)y, nip, kMagic)), pt) + y;
+        if (!(pt & 1)) d = d == (pt >> 1) ? -(pt >> 1) : d;
+        dg[e][t] = d;
+        // Insert the digit's low byte at byte t % 4 of its word.
+        dp[e][t >> 2] = (t & 3) == 0 ? d
+                                     : (int)__builtin_amdgcn_perm((uint32_t)d, (uint32_t)dp[e][t >> 2],
+                                                                   (0x03020100u & ~(0xFFu << sh)) | (0x04u << sh));
+      }
     }
   }
 
@@ -1900,35 +1998,65 @@ reconstruct_kernel(ReconArgs a) {
   double* const oblk = a.out + ((int64_t)b * a.M + (int64_t)mb * 16 + row0) * a.N + (int64_t)nb * 64;
   const uint32_t olane = 8u * (uint32_t)col;
 
-  // Horner per group of 7 (digits 7g .. 7g+6, high to low), in two int32
-  // halves: positions 6..3 give H (four balanced digits stay below 2^31;
-  // three below 2^23, so the 24-bit multiplies are exact), positions 2..0
-  // give L (|L| < 2^23); the group value is H (p_0 p_1 p_2) + L, one 32 x 32
-  // -> 64-bit multiply-add (p_i the group's first three moduli; a group of at
-  // most three digits has H = 0).
-  int h32[4][3], l32[4][3];
-#pragma unroll
-  for (int e = 0; e < 4; ++e)
-#pragma unroll
-    for (int g = 0; g < 3; ++g) { h32[e][g] = 0; l32[e][g] = 0; }
-#pragma unroll
-  for (int t = kMaxP - 1; t >= 0; --t) {
-    if (t >= P) continue;
-    const int g = t / 7, pos = t % 7;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (pos >= 3) h32[e][g] = __mul24(h32[e][g], tab_p(t)) + dg[e][t];
-      else l32[e][g] = __mul24(l32[e][g], tab_p(t)) + dg[e][t];
-    }
-  }
+  // Horner per group of 7 (digits 7g .. 7g+6, high to low), in two 32-bit
+  // halves: positions 6..3 give H, positions 2..0 give L (below 2^24), and
+  // the group value is H (p_0 p_1 p_2) + L, one 32 x 32 -> 64-bit
+  // multiply-add (p_i the group's first three moduli; a group of at most
+  // three digits has H = 0).  Every partial H below its last step is below
+  // 2^24, so the 24-bit multiplies are exact.  Balanced digits: |H| < 2^31.
+  // Default-list digits (in [0, p)): H < p_3 p_4 p_5 p_6 < 2^32 unsigned, and
+  // the group's digit offset comes off the 64-bit value.
   long long ag[4][3];
+  if constexpr (kUsual) {
+    uint32_t h32[4][3], l32[4][3];
 #pragma unroll
-  for (int g = 0; g < 3; ++g) {
-    const int t0 = 7 * g;
-    // p_0 p_1 p_2 of group g (< 2^24); moduli past P only meet H = 0.
-    const int p3 = t0 + 2 < kMaxP ? tab_p(t0) * tab_p(t0 + 1) * tab_p(t0 + 2) : 0;
+    for (int e = 0; e < 4; ++e)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) ag[e][g] = (long long)h32[e][g] * p3 + l32[e][g];
+      for (int g = 0; g < 3; ++g) { h32[e][g] = 0u; l32[e][g] = 0u; }
+#pragma unroll
+    for (int t = kMaxP - 1; t >= 0; --t) {
+      if (t >= P) continue;
+      const int g = t / 7, pos = t % 7;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (pos >= 3) h32[e][g] = __umul24(h32[e][g], (uint32_t)kDefaultModuli[t]) + (uint32_t)dg[e][t];
+        else l32[e][g] = __umul24(l32[e][g], (uint32_t)kDefaultModuli[t]) + (uint32_t)dg[e][t];
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
+      const int t0 = 7 * g;
+      const uint32_t p3 = t0 + 2 < kMaxP ? (uint32_t)(kDefaultModuli[t0] * kDefaultModuli[t0 + 1] *
+                                                      kDefaultModuli[t0 + 2]) : 0u;
+      const long long off = default_digit_offset(kP, g);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        ag[e][g] = (long long)((unsigned long long)h32[e][g] * p3 + l32[e][g]) - off;
+    }
+  } else {
+    int h32[4][3], l32[4][3];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int g = 0; g < 3; ++g) { h32[e][g] = 0; l32[e][g] = 0; }
+#pragma unroll
+    for (int t = kMaxP - 1; t >= 0; --t) {
+      if (t >= P) continue;
+      const int g = t / 7, pos = t % 7;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (pos >= 3) h32[e][g] = __mul24(h32[e][g], tab_p(t)) + dg[e][t];
+        else l32[e][g] = __mul24(l32[e][g], tab_p(t)) + dg[e][t];
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
+      const int t0 = 7 * g;
+      // p_0 p_1 p_2 of group g (< 2^24); moduli past P only meet H = 0.
+      const int p3 = t0 + 2 < kMaxP ? tab_p(t0) * tab_p(t0 + 1) * tab_p(t0 + 2) : 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ag[e][g] = (long long)h32[e][g] * p3 + l32[e][g];
+    }
   }
 
   const int ng = (P + 6) / 7;
@@ -1968,9 +2096,7 @@ reconstruct_kernel(ReconArgs a) {
       const unsigned __int128 cw =
           ((unsigned __int128)(uint64_t)(cv[e] >> (64 - cshift)) << 64) | ((uint64_t)cv[e] << cshift);
       const unsigned __int128 u = (((unsigned __int128)(uint64_t)hi << 64) | lo) + cw;
-      store_at<double>(oblk + e * a.N, olane,
-                       i128w_to_f64((uint32_t)u, (uint32_t)(u >> 32), (uint32_t)(u >> 64),
-                                    (uint32_t)(u >> 96), sh));
+      store_at<double>(oblk + e * a.N, olane, i128_to_f64((int64_t)(u >> 64), (uint64_t)u, 64 + sh));
       continue;
     } else {
       double acc = (double)(ng == 3 ? a2 : (ng == 2 ? a1 : a0));
