@@ -62,6 +62,10 @@ def parse():
                     help="only the correct-bits table of the reference's accuracy study "
                          "(six distributions x K 512/4096 at M = N = 128: native, default, "
                          "reduced) and of its default-call depths, as JSON lines")
+    ap.add_argument("--bmm-sweep", action="store_true",
+                    help="only the reference's batched grid (bench/bmmbench.py: batch x n = "
+                         "64x256 .. 4x4096): native torch.bmm, emulated bmm and a loop of "
+                         "emulated mm over the members, as JSON lines")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a float64 streaming kernel over 1 GiB (read 1 GiB, write "
                          "1 GiB) three times: the scale of the FETCH_SIZE / WRITE_SIZE counters")
@@ -100,6 +104,9 @@ def main():
         return
     if args.accuracy_grid:
         accuracy_grid()
+        return
+    if args.bmm_sweep:
+        bmm_sweep()
         return
     if args.configs:
         run_configs(max(args.steps, 3), max(args.warmup, 1),
@@ -291,6 +298,53 @@ def accuracy_grid():
                    "native": bits(A @ Bt, hi, lo),
                    "default": bits(fp64_emu.mm(A, Bt.t().contiguous()), hi, lo)}
             print(json.dumps(rec), flush=True)
+
+
+def bmm_sweep():
+    """The reference's batched grid (bench/bmmbench.py:29-43, README.md:156-172):
+    for batch x n in 64x256 .. 4x4096, randn A and B (CPU seeds), effective
+    FP64 TFLOP/s of native torch.bmm (rocBLAS), of the emulated bmm (one launch
+    chain for the batch), and of a loop of emulated mm over the members; each
+    the median of 8 event-timed calls after 3 warm-ups."""
+    import torch
+    import fp64_emu
+    dev = torch.device("cuda:0")
+    pin_rocblas()
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(8):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e-3)
+        return sorted(ts)[len(ts) // 2]
+
+    for b, n in ((64, 256), (32, 512), (16, 1024), (8, 2048), (4, 4096)):
+        g = torch.Generator().manual_seed(7000 + n)
+        A = torch.randn(b, n, n, dtype=torch.float64, generator=g).to(dev)
+        Bt = torch.randn(b, n, n, dtype=torch.float64, generator=g).to(dev)
+        Bm = Bt.transpose(1, 2).contiguous()
+        flop = 2.0 * b * n ** 3
+        tn = timed(lambda: torch.bmm(A, Bt))
+        tb = timed(lambda: fp64_emu.bmm(A, Bm))
+        tl = timed(lambda: torch.stack([fp64_emu.mm(A[i], Bm[i]) for i in range(b)]))
+        print(json.dumps({"table": "bmm_sweep", "batch": b, "n": n,
+                          "native_tflops": round(flop / tn / 1e12, 2),
+                          "emu_bmm_tflops": round(flop / tb / 1e12, 2),
+                          "emu_vs_native": round(tn / tb, 2),
+                          "looped_mm_tflops": round(flop / tl / 1e12, 2),
+                          "bmm_vs_looped": round(tl / tb, 2),
+                          "ms": {"native": round(tn * 1e3, 4), "emu_bmm": round(tb * 1e3, 4),
+                                 "looped_mm": round(tl * 1e3, 4)}}), flush=True)
+        del A, Bt, Bm
+        torch.cuda.empty_cache()
 
 
 def _config_inputs(name, torch):
