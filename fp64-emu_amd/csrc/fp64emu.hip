@@ -293,6 +293,11 @@ bool use_mixed_tiles(const fp64emu_layout_t& L) {
 
 bool use_slot_runs(const fp64emu_layout_t& L) {
   if (L.deep || L.ksplit != 1 || L.nprimes < 2 || L.Kp / kTileK > kNarrowMaxSteps) return false;
+  // One run per output tile: with fewer tiles than half the CUs, most of the
+  // chip would idle while the runs go through their slots one after another
+  // (64 x 256^3 batched: 0.173 -> 0.155 ms with one slot per group; at 128
+  // tiles the runs still win, 0.264 against 0.270 ms).
+  if (L.batch * (L.chunk_rows / kTileR) * (L.Np / kTileR) < kCUs / 2) return false;
   return !use_mixed_tiles(L);
 }
 

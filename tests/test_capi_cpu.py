@@ -273,20 +273,23 @@ def test_minimum_workspace(shape):
 
 def test_slot_runs_only_for_shallow_products():
     """Runs are chosen from the shapes alone: shallow products without a
-    K-split; deep, K-split and mixed-tile launches keep one slot per group."""
+    K-split and with output tiles for at least half the CUs; deep, K-split,
+    mixed-tile and few-tile launches keep one slot per group."""
     assert capi.layout(64, 512, 512, 512, 14, True).gemm_run == 14        # c4
     assert capi.layout(1, 8192, 8192, 8192, 14, True).gemm_run == 1       # c2: 128 k-steps
     assert capi.layout(1, 128, 128, 4096, 14, True).gemm_run == 1         # c1: K-split
     assert capi.layout(1, 300, 1290, 200, 14, True).gemm_run == 1         # mixed tiles
     assert capi.layout(1, 500, 500, 1024, 1, True).gemm_run == 1          # one modulus
+    assert capi.layout(64, 256, 256, 256, 14, True).gemm_run == 1         # 64 tiles < 128
+    assert capi.layout(128, 40, 40, 256, 14, True).gemm_run == 14         # 128 tiles
 
 
 def test_sweep_reaches_every_gemm_form():
     """The GPU sweep's shapes (tests/test_gpu_sweep.py) cover each launch
     form of the modular GEMM."""
-    from test_gpu_sweep import CASES
+    from test_gpu_sweep import CASES, RUN_CASES
     forms = set()
-    for (_, kind, batch, M, N, K, P, corr, _) in CASES:
+    for (_, kind, batch, M, N, K, P, corr, _) in CASES + RUN_CASES:
         L = capi.layout(batch, M, N, K, P, corr)
         mixed = (L.gemm_tile_cols == 256 and L.Np // 256 >= 2 and 0 < N % 256 <= 128)
         forms.add(("tile", L.gemm_tile_rows, L.gemm_tile_cols, mixed))

@@ -326,16 +326,17 @@ def test_small_tile_parity(dev, kind, batch, M, N, K):
 
 
 RUN_CASES = [
-    # kind, batch, M, N, K, moduli, corr, tile (rows, cols) -- k-steps per slot in the comment
-    ("bmm_nt", 3, 300, 200, 256, O.PRIMES[:14], True, (256, 256)),   # 4, wide tiles
-    ("bmm", 8, 512, 300, 1000, O.PRIMES[:14], True, (256, 128)),     # 16, narrow tiles
-    ("bmm", 5, 100, 90, 320, O.PRIMES[:14], True, (128, 128)),       # 5, small tiles
-    ("bmm_nt", 6, 100, 300, 50, O.PRIMES[:2], True, None),           # 1, a run of two slots
-    ("mm", 1, 700, 900, 150, O.PRIMES[:13], False, None),            # 3, odd stream of 39 steps
-    ("mm_nt", 1, 300, 256, 960, O.PRIMES[:20], True, None),          # 15, every modulus
-    ("bmm", 4, 200, 200, 200, MODULI_ORDERS[1], True, None),         # 4, even modulus 254
-    ("bmm_nt", 40, 100, 100, 64, O.PRIMES[:14], True, (128, 128)),   # 1, one tile per member
-    ("bmm", 6, 500, 260, 200, O.PRIMES[:14], True, (256, 128)),      # 4, three column tiles
+    # kind, batch, M, N, K, moduli, corr, tile (rows, cols) -- k-steps per slot in the comment.
+    # Runs need 256 x 256 output tiles for at least half the 256 CUs, hence the batch counts.
+    ("bmm_nt", 128, 300, 200, 256, O.PRIMES[:14], True, (256, 256)),   # 4, wide tiles
+    ("bmm", 64, 512, 300, 1000, O.PRIMES[:14], True, (256, 128)),      # 16, narrow tiles
+    ("bmm", 256, 100, 90, 320, O.PRIMES[:14], True, (128, 128)),       # 5, small tiles
+    ("bmm_nt", 128, 100, 300, 50, O.PRIMES[:2], True, None),           # 1, a run of two slots
+    ("mm", 1, 4000, 4000, 150, O.PRIMES[:13], False, None),            # 3, odd stream of 39 steps
+    ("bmm_nt", 256, 100, 80, 960, O.PRIMES[:20], True, None),          # 15, every modulus
+    ("bmm", 256, 200, 200, 200, MODULI_ORDERS[1], True, None),         # 4, even modulus 254
+    ("bmm_nt", 256, 100, 100, 64, O.PRIMES[:14], True, (128, 128)),    # 1, one tile per member
+    ("bmm", 64, 500, 260, 200, O.PRIMES[:14], True, (256, 128)),       # 4, three column tiles
 ]
 
 

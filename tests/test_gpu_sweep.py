@@ -2,8 +2,9 @@
 path against the CPU oracle (through the C ABI, on a pattern-filled
 workspace), for kinds, batch counts, ragged M / N / K, modulus counts,
 correction on and off and both combines drawn from a fixed generator.  The
-draws reach every GEMM launch form (256 x 256, 256 x 128, 128 x 128 and
-mixed tiles; K-splits; slot runs), as a CPU-tier test of the draws checks.
+draws, with a few many-member batched ones, reach every GEMM launch form
+(256 x 256, 256 x 128, 128 x 128 and mixed tiles; K-splits; slot runs), as a
+CPU-tier test of the draws checks.
 A second sweep draws the reference accuracy study's input distributions
 (wide exponent ranges, ill-conditioned scalings, spikes) at ragged shapes."""
 import numpy as np
@@ -37,7 +38,29 @@ def _cases():
 CASES = _cases()
 
 
-@pytest.mark.parametrize("i,kind,batch,M,N,K,P,corr,exact", CASES)
+def _run_cases():
+    """Batched products with output tiles for at least half the CUs and at
+    most 16 k-steps, the shapes that run each tile's residue slots back to back:
+    ragged members, modulus counts, correction on and off."""
+    rng = np.random.default_rng(20261204)
+    out = []
+    for i in range(6):
+        kind = ["bmm", "bmm_nt"][rng.integers(2)]
+        batch = int(rng.integers(256, 290))
+        M = int(rng.integers(1, 300 if i % 2 else 80))     # 256- and 128-row tiles
+        N = int(rng.integers(1, 80))
+        K = int(rng.integers(1, 520))
+        P = int(rng.integers(2, 21))
+        corr = bool(rng.integers(2))
+        exact = bool(rng.integers(4))
+        out.append((100 + i, kind, batch, M, N, K, P, corr, exact))
+    return out
+
+
+RUN_CASES = _run_cases()
+
+
+@pytest.mark.parametrize("i,kind,batch,M,N,K,P,corr,exact", CASES + RUN_CASES)
 def test_sweep_parity(dev, i, kind, batch, M, N, K, P, corr, exact):
     print(f"case sweep {i}: {kind} b={batch} {M}x{N}x{K} P={P} corr={corr} exact={exact}", flush=True)
     g = torch.Generator().manual_seed(5000 + i)
