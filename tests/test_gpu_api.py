@@ -241,6 +241,51 @@ def test_side_stream(dev):
     assert torch.equal(C, ref)
 
 
+def test_concurrent_host_threads(dev):
+    """Calls from several host threads, each on its own stream, give the
+    results of the same calls made one after another (the library keeps no
+    per-call state outside its workspace; the reference guards its table
+    caches with mutexes, fp64_emu_cuda/fp64_emu.cu:1038-1040)."""
+    import threading
+    print("case concurrent_host_threads", flush=True)
+    shapes = [("mm_nt", 300, 200, 700), ("mm", 129, 257, 1000), ("bmm_nt", 96, 80, 600),
+              ("mm_nt", 40, 513, 3000)]
+    inputs = []
+    for i, (kind, M, N, K) in enumerate(shapes):
+        if kind == "bmm_nt":
+            inputs.append((kind, _randn((3, M, K), 400 + i, dev), _randn((3, K, N), 410 + i, dev)))
+        elif kind == "mm":
+            inputs.append((kind, _randn((M, K), 400 + i, dev), _randn((N, K), 410 + i, dev)))
+        else:
+            inputs.append((kind, _randn((M, K), 400 + i, dev), _randn((K, N), 410 + i, dev)))
+    fn = {"mm": emu.mm, "mm_nt": emu.mm_nt, "bmm_nt": emu.bmm_nt}
+    ref = [fn[k](A, B) for k, A, B in inputs]
+    torch.cuda.synchronize()
+    out = [[None] * 3 for _ in inputs]
+    errors = []
+
+    def work(t):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for r in range(3):
+                    k, A, B = inputs[t]
+                    out[t][r] = fn[k](A, B)
+            s.synchronize()
+        except Exception as e:  # noqa: BLE001 -- reported below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(len(inputs))]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    assert not errors, errors
+    for t in range(len(inputs)):
+        for r in range(3):
+            assert torch.equal(out[t][r], ref[t]), (t, r)
+
+
 def test_mm_timed_contract(dev):
     """torch-ext/fp64_emu/__init__.py:135-149: (C, [extract, gemms, 0, reconstruct])."""
     print("case mm_timed_contract", flush=True)
