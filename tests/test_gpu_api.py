@@ -286,6 +286,24 @@ def test_concurrent_host_threads(dev):
             assert torch.equal(out[t][r], ref[t]), (t, r)
 
 
+def test_batch_beyond_reference_z_extent(dev):
+    """The reference refuses (nprimes + 2) * batch > 65535, its GEMM launch's
+    z-extent (fp64_emu_cuda/fp64_emu.cu:1652, 1680); this build's launches are
+    one-dimensional, so such a batch runs, bit-identical to the oracle."""
+    print("case batch beyond z-extent: bmm_nt 4200 x 8x8x8 and bmm 4200 x 5x7x9", flush=True)
+    assert (14 + 2) * 4200 > 65535
+    A = _randn((4200, 8, 8), 430, dev)
+    Bt = _randn((4200, 8, 8), 431, dev)
+    C = emu.bmm_nt(A, Bt, nprimes=14)
+    ref, _ = O.mm(A.cpu().numpy(), Bt.cpu().numpy(), 1, O.PRIMES[:14])
+    assert np.array_equal(C.cpu().numpy().view(np.uint64), ref.view(np.uint64))
+    A = _randn((4200, 5, 9), 432, dev)
+    B = _randn((4200, 7, 9), 433, dev)
+    C = emu.bmm(A, B, nprimes=14)
+    ref, _ = O.mm(A.cpu().numpy(), B.cpu().numpy(), 0, O.PRIMES[:14])
+    assert np.array_equal(C.cpu().numpy().view(np.uint64), ref.view(np.uint64))
+
+
 def test_mm_timed_contract(dev):
     """torch-ext/fp64_emu/__init__.py:135-149: (C, [extract, gemms, 0, reconstruct])."""
     print("case mm_timed_contract", flush=True)
