@@ -293,12 +293,23 @@ bool use_mixed_tiles(const fp64emu_layout_t& L) {
 
 bool use_slot_runs(const fp64emu_layout_t& L) {
   if (L.deep || L.ksplit != 1 || L.nprimes < 2 || L.Kp / kTileK > kNarrowMaxSteps) return false;
-  // One run per output tile: with fewer tiles than half the CUs, most of the
-  // chip would idle while the runs go through their slots one after another
-  // (64 x 256^3 batched: 0.173 -> 0.155 ms with one slot per group; at 128
-  // tiles the runs still win, 0.264 against 0.270 ms).
-  if (L.batch * (L.chunk_rows / kTileR) * (L.Np / kTileR) < kCUs / 2) return false;
   return !use_mixed_tiles(L);
+}
+
+// Residue slots per run: all P when the 256 x 256 output tiles give every CU
+// one; with fewer tiles, each tile's slots split into ceil(CUs / tiles) runs,
+// so the run groups still fill the chip (one slot per group when that leaves
+// runs of one).  A single run per tile on a few tiles left most CUs idle while
+// it went through its slots; split runs measured faster (batched 512^3: 8
+// members 0.106 -> 0.092 ms, 16 members 0.164 -> 0.151 ms; 64 x 256^3 0.161 ->
+// 0.150 ms) and no slower at 128 tiles (32 x 512^3 0.311 ms either way).
+int slot_run_length(const fp64emu_layout_t& L) {
+  const int64_t tiles = L.batch * (L.chunk_rows / kTileR) * (L.Np / kTileR);
+  if (tiles <= 0) return 1;   // empty product: no GEMM launch
+  if (tiles >= kCUs) return L.nprimes;
+  const int64_t per_tile = (kCUs + tiles - 1) / tiles;
+  const int r = (int)((L.nprimes + per_tile - 1) / per_tile);
+  return r >= 2 ? r : 1;
 }
 
 // nchunk_req > 1 (batch 1, not K-segmented): the planes of A and the output
@@ -360,7 +371,7 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   const int64_t rows128 = (std::max<int64_t>(M, 1) + 127) / 128 * 128;
   L->gemm_tile_rows = (L->gemm_tile_cols == 128 && L->nchunk == 1 && rows128 * 11 < L->Mp * 10)
                           ? 128 : 256;
-  L->gemm_run = use_slot_runs(*L) ? P : 1;
+  L->gemm_run = use_slot_runs(*L) ? slot_run_length(*L) : 1;
   // Plane rows the GEMM reads: 128-row (128-column) tiles read only the
   // first half of a 256-row plane tile past the last one holding data, so
   // the extraction skips the all-padding half there.

@@ -184,8 +184,10 @@ typedef struct {
   int gemm_tile_rows;       /* rows of one modular-GEMM output tile: 256, or 128 when
                                128-row tiles cover M with less padding too */
   int gemm_run;             /* residue slots one modular-GEMM work group runs back to back
-                               for its tile: nprimes for shallow products (at most 16
-                               k-steps, no K-split), otherwise 1 */
+                               for its tile: for shallow products (at most 16 k-steps,
+                               no K-split) nprimes when the 256 x 256 output tiles are at
+                               least 256, else nprimes split over ceil(256 / tiles) runs
+                               per tile (1 when that leaves runs of one); otherwise 1 */
   int64_t ext_rowsA;        /* rows of each A plane (per member, per row chunk) that the
                                extraction writes: the operand rows and the zero padding
                                that GEMM tiles read (a multiple of 128, at most the padded

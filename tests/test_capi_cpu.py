@@ -273,15 +273,20 @@ def test_minimum_workspace(shape):
 
 def test_slot_runs_only_for_shallow_products():
     """Runs are chosen from the shapes alone: shallow products without a
-    K-split and with output tiles for at least half the CUs; deep, K-split,
-    mixed-tile and few-tile launches keep one slot per group."""
-    assert capi.layout(64, 512, 512, 512, 14, True).gemm_run == 14        # c4
+    K-split, all P slots per run from 256 output tiles on, else split into
+    ceil(256 / tiles) runs per tile; deep, K-split, mixed-tile and very
+    few-tile launches keep one slot per group."""
+    assert capi.layout(64, 512, 512, 512, 14, True).gemm_run == 14        # c4: 256 tiles
     assert capi.layout(1, 8192, 8192, 8192, 14, True).gemm_run == 1       # c2: 128 k-steps
     assert capi.layout(1, 128, 128, 4096, 14, True).gemm_run == 1         # c1: K-split
     assert capi.layout(1, 300, 1290, 200, 14, True).gemm_run == 1         # mixed tiles
     assert capi.layout(1, 500, 500, 1024, 1, True).gemm_run == 1          # one modulus
-    assert capi.layout(64, 256, 256, 256, 14, True).gemm_run == 1         # 64 tiles < 128
-    assert capi.layout(128, 40, 40, 256, 14, True).gemm_run == 14         # 128 tiles
+    assert capi.layout(128, 40, 40, 256, 14, True).gemm_run == 7          # 128 tiles: 2 runs
+    assert capi.layout(100, 60, 70, 500, 13, False).gemm_run == 5         # 100 tiles: 3 runs
+    assert capi.layout(64, 256, 256, 256, 14, True).gemm_run == 4         # 64 tiles: 4 runs
+    assert capi.layout(40, 256, 256, 320, 20, True).gemm_run == 3         # 40 tiles: 7 runs
+    assert capi.layout(8, 512, 512, 512, 14, True).gemm_run == 2          # 32 tiles: 8 runs
+    assert capi.layout(16, 256, 256, 256, 14, True).gemm_run == 1         # 16 tiles: runs of one
 
 
 def test_sweep_reaches_every_gemm_form():

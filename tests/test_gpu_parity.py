@@ -361,3 +361,33 @@ def test_slot_run_parity(dev, kind, batch, M, N, K, primes, corr, tile):
         B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
     check_call(kind, A, B, primes, use_corr=corr)
 
+
+
+SPLIT_RUN_CASES = [
+    # kind, batch, M, N, K, moduli, corr, (tile rows, cols), expected slots per run.
+    # Fewer than 256 output tiles (in 256 x 256 units): each tile's slots split
+    # into ceil(256 / tiles) runs, the last one shorter.
+    ("bmm_nt", 70, 100, 90, 256, O.PRIMES[:14], True, (128, 128), 4),   # runs 4, 4, 4, 2
+    ("bmm", 100, 60, 70, 500, O.PRIMES[:13], False, (128, 128), 5),     # 5, 5, 3
+    ("bmm_nt", 40, 100, 120, 320, O.PRIMES[:20], True, (128, 128), 3),  # six of 3, then 2
+    ("bmm", 8, 300, 400, 256, O.PRIMES[:14], True, (256, 256), 2),      # seven of 2
+    ("bmm_nt", 32, 300, 300, 128, O.PRIMES[:14], True, (128, 128), 7),  # 7, 7
+    ("bmm", 90, 130, 100, 192, MODULI_ORDERS[1], True, (256, 128), 5),  # 5, 5, 4; even modulus 254
+]
+
+
+@pytest.mark.parametrize("kind,batch,M,N,K,primes,corr,tile,run", SPLIT_RUN_CASES)
+def test_split_slot_run_parity(dev, kind, batch, M, N, K, primes, corr, tile, run):
+    """Shallow products with fewer output tiles than CUs: each tile's residue
+    slots split over several run groups (every group starts its own operand
+    stream at its run's first plane): every stage against the oracle."""
+    from fp64_emu import capi
+    P = len(primes)
+    print(f"case split slot runs {kind} b={batch} {M}x{N}x{K} P={P} corr={corr} run={run}", flush=True)
+    L = capi.layout(batch, M, N, K, P, corr)
+    assert (L.gemm_run, L.ksplit) == (run, 1)
+    assert (L.gemm_tile_rows, L.gemm_tile_cols) == tile
+    seed = 2700 + batch + M + N + K + P
+    A = _randn((batch, M, K), seed, dev)
+    B = _randn((batch, K, N) if kind == "bmm_nt" else (batch, N, K), seed + 1, dev)
+    check_call(kind, A, B, primes, use_corr=corr)
