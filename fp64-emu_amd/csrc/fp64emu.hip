@@ -296,18 +296,22 @@ bool use_slot_runs(const fp64emu_layout_t& L) {
   return !use_mixed_tiles(L);
 }
 
-// Residue slots per run: all P when the 256 x 256 output tiles give every CU
-// one; with fewer tiles, each tile's slots split into ceil(CUs / tiles) runs,
-// so the run groups still fill the chip (one slot per group when that leaves
-// runs of one).  A single run per tile on a few tiles left most CUs idle while
-// it went through its slots; split runs measured faster (batched 512^3: 8
-// members 0.106 -> 0.092 ms, 16 members 0.164 -> 0.151 ms; 64 x 256^3 0.161 ->
-// 0.150 ms) and no slower at 128 tiles (32 x 512^3 0.311 ms either way).
+// Residue slots per run.  With fewer 256 x 256 output tiles than CUs, each
+// tile's slots split into ceil(CUs / tiles) runs, so that the run groups still
+// fill the chip: one run per tile on a few tiles left most CUs idle while it
+// went through its slots, and split runs measured faster than one slot per
+// group (batched 512^3: 8 members 0.106 -> 0.092 ms, 16 members 0.164 -> 0.151
+// ms; 64 x 256^3 0.161 -> 0.150 ms).  From a full chip on, one run of all P
+// slots per tile when the tiles fill whole rounds of CUs, else three runs per
+// tile, whose shorter groups even out the last round (batched 512^3 against
+// one run: 68 members 0.612 -> 0.559 ms, 80 members 0.685 -> 0.625 ms, 200
+// members 1.558 -> 1.513 ms; 1000 x 256^3 1.89 -> 1.85 ms; at 64 and 128
+// members, whole rounds, one run was 0.5-1% faster).  One slot per group when
+// the split leaves runs of one.
 int slot_run_length(const fp64emu_layout_t& L) {
   const int64_t tiles = L.batch * (L.chunk_rows / kTileR) * (L.Np / kTileR);
   if (tiles <= 0) return 1;   // empty product: no GEMM launch
-  if (tiles >= kCUs) return L.nprimes;
-  const int64_t per_tile = (kCUs + tiles - 1) / tiles;
+  const int64_t per_tile = tiles < kCUs ? (kCUs + tiles - 1) / tiles : (tiles % kCUs == 0 ? 1 : 3);
   const int r = (int)((L.nprimes + per_tile - 1) / per_tile);
   return r >= 2 ? r : 1;
 }

@@ -185,9 +185,10 @@ typedef struct {
                                128-row tiles cover M with less padding too */
   int gemm_run;             /* residue slots one modular-GEMM work group runs back to back
                                for its tile: for shallow products (at most 16 k-steps,
-                               no K-split) nprimes when the 256 x 256 output tiles are at
-                               least 256, else nprimes split over ceil(256 / tiles) runs
-                               per tile (1 when that leaves runs of one); otherwise 1 */
+                               no K-split) nprimes split over ceil(256 / tiles) runs per
+                               tile below 256 256 x 256 output tiles, over one run at a
+                               multiple of 256 tiles and over three runs otherwise (1
+                               when that leaves runs of one); otherwise 1 */
   int64_t ext_rowsA;        /* rows of each A plane (per member, per row chunk) that the
                                extraction writes: the operand rows and the zero padding
                                that GEMM tiles read (a multiple of 128, at most the padded

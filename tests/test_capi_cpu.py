@@ -273,9 +273,9 @@ def test_minimum_workspace(shape):
 
 def test_slot_runs_only_for_shallow_products():
     """Runs are chosen from the shapes alone: shallow products without a
-    K-split, all P slots per run from 256 output tiles on, else split into
-    ceil(256 / tiles) runs per tile; deep, K-split, mixed-tile and very
-    few-tile launches keep one slot per group."""
+    K-split, split into ceil(256 / tiles) runs per tile below 256 output tiles,
+    one run at whole multiples of 256 tiles, three runs otherwise; deep,
+    K-split, mixed-tile and very few-tile launches keep one slot per group."""
     assert capi.layout(64, 512, 512, 512, 14, True).gemm_run == 14        # c4: 256 tiles
     assert capi.layout(1, 8192, 8192, 8192, 14, True).gemm_run == 1       # c2: 128 k-steps
     assert capi.layout(1, 128, 128, 4096, 14, True).gemm_run == 1         # c1: K-split
@@ -287,6 +287,9 @@ def test_slot_runs_only_for_shallow_products():
     assert capi.layout(40, 256, 256, 320, 20, True).gemm_run == 3         # 40 tiles: 7 runs
     assert capi.layout(8, 512, 512, 512, 14, True).gemm_run == 2          # 32 tiles: 8 runs
     assert capi.layout(16, 256, 256, 256, 14, True).gemm_run == 1         # 16 tiles: runs of one
+    assert capi.layout(128, 512, 512, 512, 14, True).gemm_run == 14       # 512 tiles: whole rounds
+    assert capi.layout(80, 512, 512, 512, 14, True).gemm_run == 5         # 320 tiles: 3 runs
+    assert capi.layout(300, 256, 256, 256, 20, True).gemm_run == 7        # 300 tiles: 3 runs
 
 
 def test_sweep_reaches_every_gemm_form():
