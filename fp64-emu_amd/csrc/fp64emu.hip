@@ -237,21 +237,36 @@ void slab_split(int64_t NF, int64_t K, int64_t* kslab, int* nslab) {
 // GEMM K-split.  Output tiles x slots are the GEMM's work items; when they
 // are few against the 256 CUs (small or skinny products), S groups per tile
 // each take a contiguous K range, and reconstruction sums the S residue
-// (and correction) planes.  S minimises the estimated makespan
-// ceil(items S / 256) (k-steps per group + a fixed cost per group), keeping
-// at least 8 k-steps per group.  A function of the shapes only, so the
-// workspace size is too.
+// (and correction) planes.  S minimises an estimate of the GEMM's time plus
+// the split planes' traffic:
+//   max(ceil(items S / 256) (k-steps per group + a fixed cost per group)
+//       x the time of one k-step,  the planes' bytes / HBM rate)
+//   + S x (residue + correction bytes of one output set, written and read)
+//       / HBM rate,
+// and a larger S must gain 3%; at least 8 k-steps per group.  Without the
+// floor and the split traffic, deep skinny products split too finely
+// (512 x 512 x 20000: 16 splits 0.292 ms, 8 splits 0.281 ms; batched
+// 4 x 256 x 256 x 8192: 4 splits 0.194 ms, 2 splits 0.191 ms; 1000 x 300 x
+// 60000: 16 splits 0.944 ms, 8 splits 0.930 ms).  A function of the shapes
+// only, so the workspace size is too.
 constexpr int kCUs = 256;
 constexpr int kMaxSplit = 16;
 
-int choose_ksplit(int64_t batch, int64_t tiles, int64_t nkt, int P, int ncorr) {
+int choose_ksplit(int64_t batch, int64_t tiles, int64_t nkt, int P, int ncorr, int64_t out_elems,
+                  int64_t plane_bytes) {
+  constexpr double kStepSeconds = 0.73e-6;   // one k-step of a 256 x 256 group (8192^3)
+  constexpr double kHbmBytesPerSecond = 5.0e12;
   const int64_t items = batch * tiles * (P + (ncorr == 1 ? 2 : ncorr));  // fused corr: 2x deep
+  const double floor_s = (double)plane_bytes / kHbmBytesPerSecond;
   int best = 1;
   double best_t = 1e300;
   for (int S = 1; S <= kMaxSplit; S *= 2) {
     if (S > 1 && nkt / S < 8) break;
     const double steps = (double)((nkt + S - 1) / S) + 6.0;
-    const double t = (double)((items * S + kCUs - 1) / kCUs) * steps;
+    const double gemm = std::max((double)((items * S + kCUs - 1) / kCUs) * steps * kStepSeconds, floor_s);
+    const int nc = (S > 1 && ncorr == 1) ? 2 : ncorr;   // a K-split unfuses the correction
+    const double split = (double)S * (double)out_elems * (P + 4.0 * nc) * 2.0 / kHbmBytesPerSecond;
+    const double t = gemm + split;
     if (t < best_t * 0.97) { best_t = t; best = S; }
   }
   return best;
@@ -348,7 +363,8 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   L->memberB_bytes = (int64_t)nplanes * L->planeB_bytes;
   L->outplane_bytes = L->chunk_rows * L->Np;
   L->ksplit = L->deep ? 1 : choose_ksplit(batch, ctiles * (L->Np / kTileR), L->Kp / kTileK, P,
-                                          L->ncorr);
+                                          L->ncorr, batch * L->outplane_bytes,
+                                          batch * (L->memberA_bytes + L->memberB_bytes));
   // Under a K-split the two correction products run as two K-deep slots
   // (two int32 planes): a fused 2K-deep slot would make its groups twice as
   // long as every residue group (choose_ksplit already counts it as two).
