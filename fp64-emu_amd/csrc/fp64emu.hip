@@ -294,11 +294,16 @@ bool use_narrow_gemm(const fp64emu_layout_t& L) {
   return groups >= 2 * kCUs;
 }
 
-// Slot runs: a shallow product's groups (at most kNarrowMaxSteps k-steps per
-// slot, no K-split) each run all residue slots of their tile back to back, so
+// Slot runs: a shallow product's groups (at most kRunMaxSteps k-steps per
+// slot, no K-split) each run residue slots of their tile back to back, so
 // the operand copies stream across slots instead of every short group waiting
 // for its first stage.  Not for tiles of the mixed launch (a last tile column
-// of at most 128 columns under 256-column tiles).
+// of at most 128 columns under 256-column tiles).  The depth limit, measured
+// against one slot per group: runs gain to 32 k-steps (8 x 2048^3 batched
+// 1.56 -> 1.51 ms, 8192 x 8192 x 2048 2.47 -> 2.38 ms, 64 x 512^2 x 1536 1.17
+// -> 1.14 ms), are even at 64 (4096^3 1.136 against 1.133 ms) and lose at 128
+// (8192^3 7.22 -> 7.51 ms).
+constexpr int64_t kRunMaxSteps = 32;
 // Mixed tiles: 256-column tiles whose last tile column holds at most 128
 // columns of N run that column as 128-column tiles in the same launch.
 bool use_mixed_tiles(const fp64emu_layout_t& L) {
@@ -307,7 +312,7 @@ bool use_mixed_tiles(const fp64emu_layout_t& L) {
 }
 
 bool use_slot_runs(const fp64emu_layout_t& L) {
-  if (L.deep || L.ksplit != 1 || L.nprimes < 2 || L.Kp / kTileK > kNarrowMaxSteps) return false;
+  if (L.deep || L.ksplit != 1 || L.nprimes < 2 || L.Kp / kTileK > kRunMaxSteps) return false;
   return !use_mixed_tiles(L);
 }
 

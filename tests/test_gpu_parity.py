@@ -373,6 +373,8 @@ SPLIT_RUN_CASES = [
     ("bmm", 8, 300, 400, 256, O.PRIMES[:14], True, (256, 256), 2),      # seven of 2
     ("bmm_nt", 32, 300, 300, 128, O.PRIMES[:14], True, (128, 128), 7),  # 7, 7
     ("bmm", 90, 130, 100, 192, MODULI_ORDERS[1], True, (256, 128), 5),  # 5, 5, 4; even modulus 254
+    ("bmm_nt", 256, 16, 16, 2000, O.PRIMES[:14], True, (128, 128), 14), # 32 k-steps per slot
+    ("bmm", 40, 50, 50, 1800, O.PRIMES[:14], True, (128, 128), 2),      # 29 k-steps, seven of 2
 ]
 
 
@@ -391,3 +393,22 @@ def test_split_slot_run_parity(dev, kind, batch, M, N, K, primes, corr, tile, ru
     A = _randn((batch, M, K), seed, dev)
     B = _randn((batch, K, N) if kind == "bmm_nt" else (batch, N, K), seed + 1, dev)
     check_call(kind, A, B, primes, use_corr=corr)
+
+
+def test_deep_slot_runs_sampled(dev):
+    """Slot runs at their depth limit on 256 x 256 tiles (4096 x 4096 x 2048:
+    256 tiles, one run of 14 slots of 32 k-steps each): the sizing and
+    sampled outputs against the oracle, first and last rows and columns
+    included."""
+    from fp64_emu import capi
+    from parity_util import sampled_parity
+    n, K = 4096, 2048
+    print(f"case deep slot runs mm_nt {n}x{n}x{K} sampled", flush=True)
+    L = capi.layout(1, n, n, K, 14, True)
+    assert (L.gemm_run, L.ksplit, L.gemm_tile_rows, L.gemm_tile_cols) == (14, 1, 256, 256)
+    A = _randn((n, K), 2801, dev)
+    Bt = _randn((K, n), 2802, dev)
+    rng = np.random.default_rng(2803)
+    rows = [0, 255, 256, n - 1] + list(rng.integers(0, n, 12))
+    cols = [0, 255, 256, n - 1] + list(rng.integers(0, n, 12))
+    sampled_parity("mm_nt", A, Bt, O.PRIMES[:14], rows, cols)
