@@ -239,16 +239,20 @@ void slab_split(int64_t NF, int64_t K, int64_t* kslab, int* nslab) {
 // each take a contiguous K range, and reconstruction sums the S residue
 // (and correction) planes.  S minimises an estimate of the GEMM's time plus
 // the split planes' traffic:
-//   max(ceil(items S / 256) (k-steps per group + a fixed cost per group)
-//       x the time of one k-step,  the planes' bytes / HBM rate)
-//   + S x (residue + correction bytes of one output set, written and read)
-//       / HBM rate,
-// and a larger S must gain 3%; at least 8 k-steps per group.  Without the
-// floor and the split traffic, deep skinny products split too finely
-// (512 x 512 x 20000: 16 splits 0.292 ms, 8 splits 0.281 ms; batched
-// 4 x 256 x 256 x 8192: 4 splits 0.194 ms, 2 splits 0.191 ms; 1000 x 300 x
-// 60000: 16 splits 0.944 ms, 8 splits 0.930 ms).  A function of the shapes
-// only, so the workspace size is too.
+//   max((items S / 256 + 1/2) (k-steps per group + 3) x the time of one
+//       k-step,  the planes' bytes / HBM rate)
+//   + S x (residue + correction bytes of one output set) / HBM rate
+// (fractional rounds of groups plus half a group of tail; the split planes
+// cost their reconstruction reads, the GEMM's writes overlapping its MFMAs),
+// and a larger S must gain 3%; at least 8 k-steps per group.  Measured in one
+// process (whole calls), this picks the best S of {1, 2, 4, 8, 16} or one
+// within 2% on 16 of 17 shapes from 128 x 128 x 4096 to 8192^3 (1536^2 x
+// 4096 keeps S = 1, 4% slower than 2); the former makespan model,
+// ceil(items S / 256) (k-steps + 6), split too little at few tiles
+// (1024^2 x 4096: 0.169 against 0.154 ms at S = 2; 1024^2 x 8192: 0.307
+// against 0.264 ms) and too much for deep skinny ones (512^2 x 20000: 16
+// splits 0.292 ms, 8 splits 0.281 ms).  A function of the shapes only, so
+// the workspace size is too.
 constexpr int kCUs = 256;
 constexpr int kMaxSplit = 16;
 
@@ -262,10 +266,10 @@ int choose_ksplit(int64_t batch, int64_t tiles, int64_t nkt, int P, int ncorr, i
   double best_t = 1e300;
   for (int S = 1; S <= kMaxSplit; S *= 2) {
     if (S > 1 && nkt / S < 8) break;
-    const double steps = (double)((nkt + S - 1) / S) + 6.0;
-    const double gemm = std::max((double)((items * S + kCUs - 1) / kCUs) * steps * kStepSeconds, floor_s);
+    const double steps = (double)((nkt + S - 1) / S) + 3.0;
+    const double gemm = std::max(((double)(items * S) / kCUs + 0.5) * steps * kStepSeconds, floor_s);
     const int nc = (S > 1 && ncorr == 1) ? 2 : ncorr;   // a K-split unfuses the correction
-    const double split = (double)S * (double)out_elems * (P + 4.0 * nc) * 2.0 / kHbmBytesPerSecond;
+    const double split = (double)S * (double)out_elems * (P + 4.0 * nc) / kHbmBytesPerSecond;
     const double t = gemm + split;
     if (t < best_t * 0.97) { best_t = t; best = S; }
   }
