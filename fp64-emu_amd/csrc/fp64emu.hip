@@ -285,7 +285,7 @@ int choose_ksplit(int64_t batch, int64_t tiles, int64_t nkt, int P, int ncorr, i
 //   kNarrowMaxSteps; the fused correction slot runs twice as many) and
 //   numerous enough to give every CU two, so that groups overlap their
 //   prologues and epilogues.  Shallow products with two or more moduli run
-//   slot runs instead (use_slot_runs).
+//   slot runs on 256 x 256 tiles instead (use_slot_runs).
 constexpr int64_t kNarrowMaxSteps = 16;
 
 bool use_narrow_gemm(const fp64emu_layout_t& L) {
@@ -315,9 +315,16 @@ bool use_mixed_tiles(const fp64emu_layout_t& L) {
          L.N % kTileR <= 128;
 }
 
+// Only 256 x 256 tiles run slots: the 256 x 128 and 128 x 128 launches hold
+// two groups per CU, whose prologues and epilogues already overlap each
+// other's MFMAs, and runs there measured even or slower than one slot per
+// group (batched 16 x 1000 x 300 x 512: 0.239 against 0.212 ms; 32 x 512 x
+// 300 x 1024: 0.412 against 0.355 ms; 8192 x 640 x 2048: 0.373 against 0.325
+// ms; 128 x 128^2 x 512: 0.201 against 0.192 ms; even at 256 x 100 x 90 x 320
+// and 512 x 64^2 x 256).
 bool use_slot_runs(const fp64emu_layout_t& L) {
   if (L.deep || L.ksplit != 1 || L.nprimes < 2 || L.Kp / kTileK > kRunMaxSteps) return false;
-  return !use_mixed_tiles(L);
+  return L.gemm_tile_cols == 256 && !use_mixed_tiles(L);
 }
 
 // Residue slots per run.  With fewer 256 x 256 output tiles than CUs, each
@@ -1027,7 +1034,7 @@ struct GemmArgs {
   int64_t NB;          // 64-column output blocks per output row: Np / 64
   int P, ncorr, nslots, batch;
   int ksplit;          // groups per output tile, each over a contiguous K range
-  int run;             // residue slots per group (1, or P: one slot run per tile)
+  int run;             // residue slots per run group (1: one slot per group)
   int p[kMaxP];
   double invp[kMaxP];
 };
@@ -1115,9 +1122,10 @@ struct GemmShape {
 // XCD's L2, while all XCDs work on the same slot (whose planes then stay
 // resident in the MALL).
 //
-// With slot runs (g.run > 1) the slot index counts the correction slots, then
-// one run of g.run residue slots per tile: a group runs the run's slots
-// back to back (nrun of them) on one stream of operand copies.
+// With slot runs (g.run > 1, 256 x 256 tiles) the slot index counts the
+// correction slots, then the runs of g.run residue slots of each tile (the
+// last run of a tile shorter when g.run does not divide P): a group runs its
+// run's slots back to back (nrun of them) on one stream of operand copies.
 struct GemmItem {
   int split, slot, nrun, mt, nt;
   int64_t b;
@@ -1618,6 +1626,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
 template <bool kDeep, int kWM, int kWN, bool kRun = false>
 __global__ void __launch_bounds__(kThreads, (kWM == 8 && kWN == 8) ? 1 : 2)
 modgemm_kernel(GemmArgs g) {
+  static_assert(!kRun || (kWM == 8 && kWN == 8), "slot runs: 256 x 256 tiles only");
   using Sh = GemmShape<kWM, kWN>;
   __shared__ __attribute__((aligned(1024))) int8_t lds[Sh::kS * Sh::kSB];
   const GemmItem it = gemm_item(g);
@@ -2478,11 +2487,7 @@ int run(const Call& c) {
       ga.first = seg == 0 ? 1 : 0;
       if (L.deep)
         hipLaunchKernelGGL((modgemm_kernel<true, 8, 8>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
-      else if (ga.run > 1 && small)
-        hipLaunchKernelGGL((modgemm_kernel<false, 4, 4, true>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
-      else if (ga.run > 1 && narrow)
-        hipLaunchKernelGGL((modgemm_kernel<false, 8, 4, true>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
-      else if (ga.run > 1)
+      else if (ga.run > 1)   // 256 x 256 tiles only (use_slot_runs)
         hipLaunchKernelGGL((modgemm_kernel<false, 8, 8, true>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       else if (small)
         hipLaunchKernelGGL((modgemm_kernel<false, 4, 4>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);

@@ -184,8 +184,9 @@ typedef struct {
   int gemm_tile_rows;       /* rows of one modular-GEMM output tile: 256, or 128 when
                                128-row tiles cover M with less padding too */
   int gemm_run;             /* residue slots one modular-GEMM work group runs back to back
-                               for its tile: for shallow products (at most 32 k-steps,
-                               no K-split) nprimes split over ceil(256 / tiles) runs per
+                               for its tile: for shallow products on 256 x 256 tiles
+                               (at most 32 k-steps, no K-split) nprimes split over
+                               ceil(256 / tiles) runs per
                                tile below 256 256 x 256 output tiles, over one run at a
                                multiple of 256 tiles and over three runs otherwise (1
                                when that leaves runs of one); otherwise 1 */

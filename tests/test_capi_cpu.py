@@ -273,16 +273,20 @@ def test_minimum_workspace(shape):
 
 def test_slot_runs_only_for_shallow_products():
     """Runs are chosen from the shapes alone: shallow products without a
-    K-split, split into ceil(256 / tiles) runs per tile below 256 output tiles,
-    one run at whole multiples of 256 tiles, three runs otherwise; deep,
-    K-split, mixed-tile and very few-tile launches keep one slot per group."""
+    K-split on 256 x 256 tiles, split into ceil(256 / tiles) runs per tile
+    below 256 output tiles, one run at whole multiples of 256 tiles, three
+    runs otherwise; deep, K-split, mixed-tile, 256 x 128 or 128 x 128 tile and
+    very few-tile launches keep one slot per group."""
     assert capi.layout(64, 512, 512, 512, 14, True).gemm_run == 14        # c4: 256 tiles
     assert capi.layout(1, 8192, 8192, 8192, 14, True).gemm_run == 1       # c2: 128 k-steps
     assert capi.layout(1, 128, 128, 4096, 14, True).gemm_run == 1         # c1: K-split
     assert capi.layout(1, 300, 1290, 200, 14, True).gemm_run == 1         # mixed tiles
     assert capi.layout(1, 500, 500, 1024, 1, True).gemm_run == 1          # one modulus
-    assert capi.layout(128, 40, 40, 256, 14, True).gemm_run == 7          # 128 tiles: 2 runs
-    assert capi.layout(100, 60, 70, 500, 13, False).gemm_run == 5         # 100 tiles: 3 runs
+    assert capi.layout(32, 500, 500, 128, 14, True).gemm_run == 7         # 128 tiles: 2 runs
+    assert capi.layout(1, 2560, 2560, 200, 13, False).gemm_run == 5       # 100 tiles: 3 runs
+    # 256 x 128 and 128 x 128 tiles (two groups per CU) keep one slot per group
+    assert capi.layout(128, 40, 40, 256, 14, True).gemm_run == 1
+    assert capi.layout(64, 512, 300, 1000, 14, True).gemm_run == 1
     assert capi.layout(64, 256, 256, 256, 14, True).gemm_run == 4         # 64 tiles: 4 runs
     assert capi.layout(40, 256, 256, 320, 20, True).gemm_run == 3         # 40 tiles: 7 runs
     assert capi.layout(8, 512, 512, 512, 14, True).gemm_run == 2          # 32 tiles: 8 runs

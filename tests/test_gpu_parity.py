@@ -327,16 +327,14 @@ def test_small_tile_parity(dev, kind, batch, M, N, K):
 
 RUN_CASES = [
     # kind, batch, M, N, K, moduli, corr, tile (rows, cols) -- k-steps per slot in the comment.
-    # Runs need 256 x 256 output tiles for at least half the 256 CUs, hence the batch counts.
-    ("bmm_nt", 128, 300, 200, 256, O.PRIMES[:14], True, (256, 256)),   # 4, wide tiles
-    ("bmm", 64, 512, 300, 1000, O.PRIMES[:14], True, (256, 128)),      # 16, narrow tiles
-    ("bmm", 256, 100, 90, 320, O.PRIMES[:14], True, (128, 128)),       # 5, small tiles
-    ("bmm_nt", 128, 100, 300, 50, O.PRIMES[:2], True, None),           # 1, a run of two slots
+    # One run of every residue slot per tile: 256 x 256 output tiles in whole rounds of the
+    # 256 CUs, hence the batch counts and sizes.
+    ("bmm_nt", 128, 300, 200, 256, O.PRIMES[:14], True, (256, 256)),   # 4
     ("mm", 1, 4000, 4000, 150, O.PRIMES[:13], False, None),            # 3, odd stream of 39 steps
-    ("bmm_nt", 256, 100, 80, 960, O.PRIMES[:20], True, None),          # 15, every modulus
+    ("mm_nt", 1, 4096, 4096, 64, O.PRIMES[:20], True, (256, 256)),     # 1, every modulus
+    ("mm", 1, 4096, 4096, 50, O.PRIMES[:2], True, None),               # 1, a run of two slots
     ("bmm", 256, 200, 200, 200, MODULI_ORDERS[1], True, None),         # 4, even modulus 254
-    ("bmm_nt", 256, 100, 100, 64, O.PRIMES[:14], True, (128, 128)),    # 1, one tile per member
-    ("bmm", 64, 500, 260, 200, O.PRIMES[:14], True, (256, 128)),       # 4, three column tiles
+    ("bmm_nt", 256, 240, 250, 64, O.PRIMES[:14], True, (256, 256)),   # 1, one tile per member
 ]
 
 
@@ -365,24 +363,25 @@ def test_slot_run_parity(dev, kind, batch, M, N, K, primes, corr, tile):
 
 SPLIT_RUN_CASES = [
     # kind, batch, M, N, K, moduli, corr, (tile rows, cols), expected slots per run.
-    # Fewer than 256 output tiles (in 256 x 256 units): each tile's slots split
-    # into ceil(256 / tiles) runs, the last one shorter.
-    ("bmm_nt", 70, 100, 90, 256, O.PRIMES[:14], True, (128, 128), 4),   # runs 4, 4, 4, 2
-    ("bmm", 100, 60, 70, 500, O.PRIMES[:13], False, (128, 128), 5),     # 5, 5, 3
-    ("bmm_nt", 40, 100, 120, 320, O.PRIMES[:20], True, (128, 128), 3),  # six of 3, then 2
-    ("bmm", 8, 300, 400, 256, O.PRIMES[:14], True, (256, 256), 2),      # seven of 2
-    ("bmm_nt", 32, 300, 300, 128, O.PRIMES[:14], True, (128, 128), 7),  # 7, 7
-    ("bmm", 90, 130, 100, 192, MODULI_ORDERS[1], True, (256, 128), 5),  # 5, 5, 4; even modulus 254
-    ("bmm_nt", 256, 16, 16, 2000, O.PRIMES[:14], True, (128, 128), 14), # 32 k-steps per slot
-    ("bmm", 40, 50, 50, 1800, O.PRIMES[:14], True, (128, 128), 2),      # 29 k-steps, seven of 2
+    # Fewer than 256 output tiles: each tile's slots split into ceil(256 / tiles)
+    # runs, the last one shorter; past 256 tiles and off whole rounds, three runs.
+    ("mm_nt", 1, 1792, 2560, 256, O.PRIMES[:14], True, (256, 256), 4),  # 70 tiles: 4, 4, 4, 2
+    ("mm", 1, 2560, 2560, 200, O.PRIMES[:13], False, (256, 256), 5),    # 100 tiles: 5, 5, 3
+    ("mm_nt", 1, 1280, 2048, 320, O.PRIMES[:20], True, (256, 256), 3),  # 40 tiles: six of 3, then 2
+    ("bmm", 8, 300, 400, 256, O.PRIMES[:14], True, (256, 256), 2),      # 32 tiles: seven of 2
+    ("bmm_nt", 32, 500, 500, 128, O.PRIMES[:14], True, (256, 256), 7),  # 128 tiles: 7, 7
+    ("bmm", 90, 240, 250, 192, MODULI_ORDERS[1], True, (256, 256), 5),  # 5, 5, 4; even modulus 254
+    ("bmm", 20, 240, 240, 1800, O.PRIMES[:14], True, (256, 256), 2),    # 29 k-steps per slot
+    ("bmm_nt", 300, 240, 250, 64, O.PRIMES[:14], True, (256, 256), 5),  # 300 tiles: three runs
 ]
 
 
 @pytest.mark.parametrize("kind,batch,M,N,K,primes,corr,tile,run", SPLIT_RUN_CASES)
 def test_split_slot_run_parity(dev, kind, batch, M, N, K, primes, corr, tile, run):
-    """Shallow products with fewer output tiles than CUs: each tile's residue
-    slots split over several run groups (every group starts its own operand
-    stream at its run's first plane): every stage against the oracle."""
+    """Shallow products whose output tiles do not fill whole rounds of CUs:
+    each tile's residue slots split over several run groups (every group
+    starts its own operand stream at its run's first plane): every stage
+    against the oracle."""
     from fp64_emu import capi
     P = len(primes)
     print(f"case split slot runs {kind} b={batch} {M}x{N}x{K} P={P} corr={corr} run={run}", flush=True)
@@ -390,8 +389,12 @@ def test_split_slot_run_parity(dev, kind, batch, M, N, K, primes, corr, tile, ru
     assert (L.gemm_run, L.ksplit) == (run, 1)
     assert (L.gemm_tile_rows, L.gemm_tile_cols) == tile
     seed = 2700 + batch + M + N + K + P
-    A = _randn((batch, M, K), seed, dev)
-    B = _randn((batch, K, N) if kind == "bmm_nt" else (batch, N, K), seed + 1, dev)
+    if kind in ("bmm", "bmm_nt"):
+        A = _randn((batch, M, K), seed, dev)
+        B = _randn((batch, K, N) if kind == "bmm_nt" else (batch, N, K), seed + 1, dev)
+    else:
+        A = _randn((M, K), seed, dev)
+        B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
     check_call(kind, A, B, primes, use_corr=corr)
 
 
