@@ -184,12 +184,12 @@ typedef struct {
   int gemm_tile_rows;       /* rows of one modular-GEMM output tile: 256, or 128 when
                                128-row tiles cover M with less padding too */
   int gemm_run;             /* residue slots one modular-GEMM work group runs back to back
-                               for its tile: for shallow products on 256 x 256 tiles
-                               (at most 32 k-steps, no K-split) nprimes split over
-                               ceil(256 / tiles) runs per
-                               tile below 256 256 x 256 output tiles, over one run at a
-                               multiple of 256 tiles and over three runs otherwise (1
-                               when that leaves runs of one); otherwise 1 */
+                               for its tile; 1 (one slot per group) except for shallow
+                               products on 256 x 256 tiles (at most 32 k-steps, no
+                               K-split), whose nprimes slots split over ceil(256 / T)
+                               runs per tile when the T output tiles are fewer than
+                               256, one run when T is a multiple of 256 and three runs
+                               otherwise (1 when that leaves runs of one) */
   int64_t ext_rowsA;        /* rows of each A plane (per member, per row chunk) that the
                                extraction writes: the operand rows and the zero padding
                                that GEMM tiles read (a multiple of 128, at most the padded
