@@ -109,6 +109,33 @@ def test_layout_consistency(shape, P, corr):
     assert capi.workspace_size(batch, M, N, K, P, corr) == L.total
 
 
+def test_layout_choices_fuzz():
+    """The layout's launch choices over 3000 seeded shapes (log-uniform
+    sizes, batches, depths through the K-segmented range, every modulus
+    count, correction on and off): no failure, and each choice within the
+    ranges the GEMM launches assume."""
+    rng = np.random.default_rng(20261206)
+    for _ in range(3000):
+        batch = int(np.exp(rng.uniform(0, np.log(2000)))) if rng.random() < 0.5 else 1
+        M = int(np.exp(rng.uniform(0, np.log(20000))))
+        N = int(np.exp(rng.uniform(0, np.log(20000))))
+        K = int(np.exp(rng.uniform(0, np.log(400000))))
+        if batch * M * K > 2 ** 33 or batch * N * K > 2 ** 33:
+            continue
+        P = int(rng.integers(1, 21))
+        corr = bool(rng.integers(2))
+        L = capi.layout(batch, M, N, K, P, corr)
+        case = (batch, M, N, K, P, corr)
+        assert L.ksplit in (1, 2, 4, 8, 16), case
+        assert L.ksplit == 1 or (not L.deep and (L.Kp // 64) // L.ksplit >= 8), case
+        assert 1 <= L.gemm_run <= max(P, 1), case
+        if L.gemm_run > 1:
+            assert (L.gemm_tile_rows, L.gemm_tile_cols, L.ksplit, L.deep) == (256, 256, 1, 0), case
+            assert L.Kp // 64 <= 32 and P >= 2, case
+        assert (L.gemm_tile_rows, L.gemm_tile_cols) in ((256, 256), (256, 128), (128, 128)), case
+        assert capi.workspace_size_min(batch, M, N, K, P, corr) <= L.total, case
+
+
 def test_layout_rejects_bad_arguments():
     with pytest.raises(capi.CapiError):
         capi.layout(1, -1, 4, 4, 14, True)
