@@ -378,9 +378,10 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   L->memberA_bytes = (int64_t)nplanes * L->planeA_bytes;
   L->memberB_bytes = (int64_t)nplanes * L->planeB_bytes;
   L->outplane_bytes = L->chunk_rows * L->Np;
-  L->ksplit = L->deep ? 1 : choose_ksplit(batch, ctiles * (L->Np / kTileR), L->Kp / kTileK, P,
-                                          L->ncorr, batch * L->outplane_bytes,
-                                          batch * (L->memberA_bytes + L->memberB_bytes));
+  // (K-segmented: per segment launch; each split keeps its own int32 residue
+  // and int64 correction sums across the segments.)
+  L->ksplit = choose_ksplit(batch, ctiles * (L->Np / kTileR), L->Kp / kTileK, P, L->ncorr,
+                            batch * L->outplane_bytes, batch * (L->memberA_bytes + L->memberB_bytes));
   // Under a K-split the two correction products run as two K-deep slots
   // (two int32 planes): a fused 2K-deep slot would make its groups twice as
   // long as every residue group (choose_ksplit already counts it as two).
@@ -1529,7 +1530,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   } else if (kDeep && is_corr) {
     // K-segmented: this segment's correction products join the int64 sum.
     typedef long long v2l __attribute__((ext_vector_type(2)));
-    int64_t* dst = g.cacc + b * g.outplane;
+    int64_t* dst = g.cacc + (((int64_t)split * g.batch + b) * g.ncorr + slot) * g.outplane;
 #pragma unroll
     for (int x = 0; x < kWM; ++x)
 #pragma unroll
@@ -1554,7 +1555,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     // bal8's range [-(p/2 - 1), p/2] for even p (for p = 256 the same bytes).
     const bool tie_fix = !(g.p[t] & 1) && g.p[t] != 256;
     const int half_lo = -(g.p[t] >> 1);
-    int32_t* dst = g.racc + (b * g.P + t) * g.outplane;
+    int32_t* dst = g.racc + (((int64_t)split * g.batch + b) * g.P + t) * g.outplane;
 #pragma unroll
     for (int x = 0; x < kWM; ++x)
 #pragma unroll
@@ -1843,21 +1844,27 @@ reconstruct_kernel(ReconArgs a) {
   uint32_t w[kMaxP];
   int64_t cv[4] = {0, 0, 0, 0};
   if (kDeep) {
-    // Fold the segment sums (|sum| <= 128 per segment) to balanced residues.
+    // Fold the segment sums (|sum| <= 128 per segment and split) to balanced
+    // residues; the S splits' sums add first, and so do their correction
+    // sums (S x ncorr int64 planes).
+    const int64_t sstride = (int64_t)a.batch * P * a.outplane;
 #pragma unroll
     for (int t = 0; t < kMaxP; ++t)
       if (t < P) {
-        const v4i v = *reinterpret_cast<const v4i*>(a.res32 + (b * P + t) * a.outplane + boff);
+        const int32_t* r = a.res32 + (b * P + t) * a.outplane + boff;
+        v4i v = *reinterpret_cast<const v4i*>(r);
+        for (int sp = 1; sp < a.ksplit; ++sp) v += *reinterpret_cast<const v4i*>(r + sp * sstride);
         const double ip = a.tab.invp[t];
         const int negp = -a.tab.p[t];
         w[t] = pack_bytes(acc_residue(v[0], ip, negp), acc_residue(v[1], ip, negp),
                           acc_residue(v[2], ip, negp), acc_residue(v[3], ip, negp));
       }
-    if (a.ncorr > 0) {
-      const int64_t* c = a.corr64 + b * a.outplane + boff;
+    for (int sp = 0; sp < a.ksplit; ++sp)
+      for (int cc = 0; cc < a.ncorr; ++cc) {
+        const int64_t* c = a.corr64 + (((int64_t)sp * a.batch + b) * a.ncorr + cc) * a.outplane + boff;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) cv[e] = c[e];
-    }
+        for (int e = 0; e < 4; ++e) cv[e] += c[e];
+      }
   } else if (!kSplit) {
     const int8_t* rb = a.res8 + (int64_t)b * P * a.outplane + boff0;
 #pragma unroll

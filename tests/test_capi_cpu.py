@@ -80,7 +80,7 @@ def test_layout_consistency(shape, P, corr):
     deep = K > 131071
     assert L.deep == int(deep) and L.nseg == ((K + 65535) // 65536 if deep else 1)
     assert L.kseg == (65536 if deep else K)
-    assert L.ncorr == (0 if not corr else (1 if (deep or (K <= 65536 and L.ksplit == 1)) else 2))
+    assert L.ncorr == (0 if not corr else (1 if (L.ksplit == 1 and (deep or K <= 65536)) else 2))
     nplanes = P + (2 if corr else 0)
     assert L.planeA_bytes == L.Mp * L.Kp and L.planeB_bytes == L.Np * L.Kp
     assert L.memberA_bytes == nplanes * L.planeA_bytes
@@ -97,8 +97,8 @@ def test_layout_consistency(shape, P, corr):
              ("off_lgB", 4 * batch * N), ("off_bits", 16), ("off_pmax", 8 * L.nslab * batch * N),
              ("off_pss", 8 * L.nslab * batch * N), ("off_planesA", batch * L.memberA_bytes),
              ("off_planesB", batch * L.memberB_bytes),
-             ("off_res8", (4 if deep else 1) * batch * P * L.outplane_bytes),
-             ("off_corr", (8 if deep else 4) * batch * L.ncorr * L.outplane_bytes)]
+             ("off_res8", (4 if deep else 1) * L.ksplit * batch * P * L.outplane_bytes),
+             ("off_corr", (8 if deep else 4) * L.ksplit * batch * L.ncorr * L.outplane_bytes)]
     prev_end = 0
     for name, size in sizes:
         off = getattr(L, name)
@@ -127,7 +127,7 @@ def test_layout_choices_fuzz():
         L = capi.layout(batch, M, N, K, P, corr)
         case = (batch, M, N, K, P, corr)
         assert L.ksplit in (1, 2, 4, 8, 16), case
-        assert L.ksplit == 1 or (not L.deep and (L.Kp // 64) // L.ksplit >= 8), case
+        assert L.ksplit == 1 or (L.Kp // 64) // L.ksplit >= 8, case
         assert 1 <= L.gemm_run <= max(P, 1), case
         if L.gemm_run > 1:
             assert (L.gemm_tile_rows, L.gemm_tile_cols, L.ksplit, L.deep) == (256, 256, 1, 0), case
