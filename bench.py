@@ -66,6 +66,9 @@ def parse():
                     help="only the reference's batched grid (bench/bmmbench.py: batch x n = "
                          "64x256 .. 4x4096): native torch.bmm, emulated bmm and a loop of "
                          "emulated mm over the members, as JSON lines")
+    ap.add_argument("--square-sweep", action="store_true",
+                    help="only square mm_nt products n = 1000 .. 10000 (not multiples of the "
+                         "tile size): native float64 matmul against the emulation, as JSON lines")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a float64 streaming kernel over 1 GiB (read 1 GiB, write "
                          "1 GiB) three times: the scale of the FETCH_SIZE / WRITE_SIZE counters")
@@ -107,6 +110,9 @@ def main():
         return
     if args.bmm_sweep:
         bmm_sweep()
+        return
+    if args.square_sweep:
+        square_sweep()
         return
     if args.configs:
         run_configs(max(args.steps, 3), max(args.warmup, 1),
@@ -298,6 +304,49 @@ def accuracy_grid():
                    "native": bits(A @ Bt, hi, lo),
                    "default": bits(fp64_emu.mm(A, Bt.t().contiguous()), hi, lo)}
             print(json.dumps(rec), flush=True)
+
+
+def _median_event_time(fn, torch, reps=8):
+    """Median of `reps` event-timed calls of fn after 3 warm-ups, in seconds."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e-3)
+    return sorted(ts)[len(ts) // 2]
+
+
+def square_sweep():
+    """Square mm_nt products of sizes that are not multiples of the GEMM tile
+    (randn A and Bt, CPU seeds 9500 + n): native float64 matmul (rocBLAS)
+    against the emulation at the default plan, each the median of 8
+    event-timed calls after 3 warm-ups."""
+    import torch
+    import fp64_emu
+    dev = torch.device("cuda:0")
+    pin_rocblas()
+    for n in (1000, 1500, 2000, 3000, 5000, 6000, 10000):
+        g = torch.Generator().manual_seed(9500 + n)
+        A = torch.randn((n, n), dtype=torch.float64, generator=g).to(dev)
+        Bt = torch.randn((n, n), dtype=torch.float64, generator=g).to(dev)
+        flop = 2.0 * n ** 3
+        tn = _median_event_time(lambda: A @ Bt, torch)
+        te = _median_event_time(lambda: fp64_emu.mm_nt(A, Bt), torch)
+        print(json.dumps({"table": "square_sweep", "n": n,
+                          "native_tflops": round(flop / tn / 1e12, 2),
+                          "emu_tflops": round(flop / te / 1e12, 2),
+                          "emu_vs_native": round(tn / te, 2),
+                          "ms": {"native": round(tn * 1e3, 4), "emu": round(te * 1e3, 4)}}),
+              flush=True)
+        del A, Bt
+        torch.cuda.empty_cache()
 
 
 def bmm_sweep():
