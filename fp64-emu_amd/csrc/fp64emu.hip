@@ -291,7 +291,21 @@ constexpr int64_t kNarrowMaxSteps = 16;
 bool use_narrow_gemm(const fp64emu_layout_t& L) {
   if (L.deep) return false;
   const int64_t cols128 = (L.N + 127) / 128 * 128;
-  if (cols128 * 11 < L.Np * 10) return true;
+  const int64_t rows128 = (std::max<int64_t>(L.M, 1) + 127) / 128 * 128;
+  // 128-column tiles save padded work (> ~9%).  Deep products (128 k-steps
+  // and more) whose groups stay deep after the K-split (64 k-steps and
+  // more), where the narrow loop's extra operand traffic per operation tells,
+  // take them only with 128-row tiles too (128 x 128: M padded less as well)
+  // or a saving of 40% and more.  Measured at K = 8192: 2048 x 300, 2048 x
+  // 640 and 4096 x 384 (two splits of 64 k-steps) ran 5-8% faster on 256 x
+  // 256 tiles, 300 x 300 to 640 x 1152 7-13% faster on 128 x 128 tiles;
+  // 512 x 384 x 20000 (eight splits of 40) 7% faster on the narrow tiles; at
+  // K <= 4096 the narrow tiles won or tied.
+  const int64_t nkt = L.Kp / kTileK;
+  const bool rows_save = L.nchunk == 1 && rows128 * 11 < L.Mp * 10;
+  const bool deep_groups = nkt >= 128 && (nkt + L.ksplit - 1) / L.ksplit >= 64;
+  if (cols128 * 11 < L.Np * 10 && (rows_save || !deep_groups || cols128 * 5 <= L.Np * 3))
+    return true;
   if (L.ksplit != 1 || L.Kp / kTileK > kNarrowMaxSteps || L.nprimes >= 2) return false;
   const int64_t groups = (int64_t)(L.nprimes + L.ncorr) * L.batch * (L.chunk_rows / kTileR) *
                          (cols128 / 128);
