@@ -2407,8 +2407,8 @@ int run(const Call& c) {
   ga.memberA = L.memberA_bytes; ga.memberB = L.memberB_bytes;
   ga.planeA = L.planeA_bytes; ga.planeB = L.planeB_bytes;
   ga.outplane = L.outplane_bytes;
-  // Shallow products with many groups run the narrow kernel (two groups per
-  // CU); its column tiles past N hold only padding and are not launched.
+  // 128-column (narrow) and 128 x 128 (small) tiles run two groups per CU;
+  // their column tiles past N hold only padding and are not launched.
   const bool narrow = L.gemm_tile_cols == 128;
   const bool small = narrow && L.gemm_tile_rows == 128;
   // Wide tiles whose last tile column holds at most 128 columns of N: that
