@@ -285,7 +285,8 @@ int choose_ksplit(int64_t batch, int64_t tiles, int64_t nkt, int P, int ncorr, i
 //   kNarrowMaxSteps; the fused correction slot runs twice as many) and
 //   numerous enough to give every CU two, so that groups overlap their
 //   prologues and epilogues.  Shallow products with two or more moduli run
-//   slot runs on 256 x 256 tiles instead (use_slot_runs).
+//   slot runs on 256 x 256 tiles instead (use_slot_runs) when they have a
+//   256 x 256 tile per CU, and narrow tiles otherwise (make_layout).
 constexpr int64_t kNarrowMaxSteps = 16;
 
 bool use_narrow_gemm(const fp64emu_layout_t& L) {
@@ -341,22 +342,18 @@ bool use_slot_runs(const fp64emu_layout_t& L) {
   return L.gemm_tile_cols == 256 && !use_mixed_tiles(L);
 }
 
-// Residue slots per run.  With fewer 256 x 256 output tiles than CUs, each
-// tile's slots split into ceil(CUs / tiles) runs, so that the run groups still
-// fill the chip: one run per tile on a few tiles left most CUs idle while it
-// went through its slots, and split runs measured faster than one slot per
-// group (batched 512^3: 8 members 0.106 -> 0.092 ms, 16 members 0.164 -> 0.151
-// ms; 64 x 256^3 0.161 -> 0.150 ms).  From a full chip on, one run of all P
-// slots per tile when the tiles fill whole rounds of CUs, else three runs per
-// tile, whose shorter groups even out the last round (batched 512^3 against
-// one run: 68 members 0.612 -> 0.559 ms, 80 members 0.685 -> 0.625 ms, 200
-// members 1.558 -> 1.513 ms; 1000 x 256^3 1.89 -> 1.85 ms; at 64 and 128
-// members, whole rounds, one run was 0.5-1% faster).  One slot per group when
-// the split leaves runs of one.
+// Residue slots per run.  Slot runs reach only products of at least one
+// 256 x 256 output tile per CU (fewer tiles take 256 x 128 or 128 x 128 tiles
+// in make_layout).  One run of all P slots per tile when the tiles fill whole
+// rounds of CUs, else three runs per tile, whose shorter groups even out the
+// last round (batched 512^3 against one run: 68 members 0.612 -> 0.559 ms, 80
+// members 0.685 -> 0.625 ms, 200 members 1.558 -> 1.513 ms; 1000 x 256^3 1.89
+// -> 1.85 ms; at 64 and 128 members, whole rounds, one run was 0.5-1%
+// faster).  One slot per group when the split leaves runs of one.
 int slot_run_length(const fp64emu_layout_t& L) {
   const int64_t tiles = L.batch * (L.chunk_rows / kTileR) * (L.Np / kTileR);
   if (tiles <= 0) return 1;   // empty product: no GEMM launch
-  const int64_t per_tile = tiles < kCUs ? (kCUs + tiles - 1) / tiles : (tiles % kCUs == 0 ? 1 : 3);
+  const int64_t per_tile = tiles % kCUs == 0 ? 1 : 3;
   const int r = (int)((L.nprimes + per_tile - 1) / per_tile);
   return r >= 2 ? r : 1;
 }
@@ -422,6 +419,23 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   const int64_t rows128 = (std::max<int64_t>(M, 1) + 127) / 128 * 128;
   L->gemm_tile_rows = (L->gemm_tile_cols == 128 && L->nchunk == 1 && rows128 * 11 < L->Mp * 10)
                           ? 128 : 256;
+  // Shallow products (at most kRunMaxSteps k-steps, no K-split, two moduli or
+  // more) with fewer 256 x 256 output tiles than CUs run one slot per group
+  // on 256 x 128 tiles, two groups per CU (128 x 128 tiles at 40 tiles or
+  // fewer): measured against 256 x 256 tiles in runs split to fill the chip,
+  // 3-18% faster on 17 of 19 shapes from 512^3 and batched 8 x 512^3 to
+  // 3584^2 x 1536 (e.g. 2 x 2048^3 batched 0.506 -> 0.421 ms, 3072^2 x 1024
+  // 0.302 -> 0.257 ms, 1500^3 0.147 -> 0.121 ms on 128 x 128), even on the
+  // other two; from 256 tiles on the 256 x 256 runs stay faster (c4 0.490
+  // against 0.516 ms, 80 x 512^3 0.620 against 0.627 ms).
+  {
+    const int64_t tiles = batch * (L->chunk_rows / kTileR) * (L->Np / kTileR);
+    if (!L->deep && L->ksplit == 1 && P >= 2 && L->Kp / kTileK <= kRunMaxSteps && tiles > 0 &&
+        tiles < kCUs) {
+      L->gemm_tile_cols = 128;
+      if (L->nchunk == 1 && tiles <= 40) L->gemm_tile_rows = 128;
+    }
+  }
   L->gemm_run = use_slot_runs(*L) ? slot_run_length(*L) : 1;
   // Plane rows the GEMM reads: 128-row (128-column) tiles read only the
   // first half of a 256-row plane tile past the last one holding data, so

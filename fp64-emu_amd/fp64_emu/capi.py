@@ -123,21 +123,34 @@ def run(kind, A, B, primes, exact=True, bits=53, use_corr=True, out=None, ws=Non
     primes = np.ascontiguousarray(np.asarray(primes, dtype=np.int32))
     P = int(primes.size)
     batched = kind in ("bmm", "bmm_nt")
+    nt = kind.endswith("_nt")
+    # The C entry points take bare pointers: every extent they read is checked
+    # here against the tensors, before any launch.
+    if A.dim() != (3 if batched else 2) or B.dim() != A.dim():
+        raise ValueError(f"{kind}: operands of {A.dim()} and {B.dim()} dims")
     if batched:
         batch, M, K = A.shape
-        N = B.shape[2] if kind == "bmm_nt" else B.shape[1]
+        if B.shape[0] != batch:
+            raise ValueError(f"{kind}: batch {batch} against {B.shape[0]}")
     else:
         batch = 1
         M, K = A.shape
-        N = B.shape[1] if kind == "mm_nt" else B.shape[0]
+    KB, N = (B.shape[-2], B.shape[-1]) if nt else (B.shape[-1], B.shape[-2])
+    if KB != K:
+        raise ValueError(f"{kind}: K of A is {K}, of B {KB} (B {tuple(B.shape)})")
+    for name, t in (("A", A), ("B", B)):
+        if t.dtype != torch.float64 or not t.is_contiguous() or t.device != A.device:
+            raise ValueError(f"{kind}: {name} must be contiguous float64 on {A.device}")
     lay = layout(batch, M, N, K, P, use_corr)
     if ws is None:
         ws = torch.empty(max(int(lay.total), 1), dtype=torch.uint8, device=A.device)
         if fill is not None:
             ws.fill_(fill)
+    shape = (batch, M, N) if batched else (M, N)
     if out is None:
-        shape = (batch, M, N) if batched else (M, N)
         out = torch.empty(shape, dtype=torch.float64, device=A.device)
+    elif tuple(out.shape) != shape or out.dtype != torch.float64 or not out.is_contiguous():
+        raise ValueError(f"{kind}: out must be contiguous float64 of shape {shape}")
     pp = primes.ctypes.data_as(ctypes.c_void_p)
     fn = getattr(lib(), "fp64emu_" + kind)
     common = (pp, None, None, P, int(bool(exact)), int(bits), int(bool(use_corr)),

@@ -177,19 +177,22 @@ typedef struct {
   size_t off_sftA, off_sftB, off_lgA, off_lgB, off_bits, off_pmax, off_pss;
   size_t off_planesA, off_planesB, off_res8, off_corr, total;
   int gemm_tile_cols;       /* columns of one modular-GEMM output tile: 256, or 128 where
-                               128 columns cover N with less padding, or for a single
+                               128 columns cover N with less padding, for a single
                                modulus in shallow products with many tiles (two work
-                               groups per CU; shallow products with more moduli run
-                               slot runs) */
+                               groups per CU), or for shallow products with more moduli
+                               and fewer than 256 tiles of 256 x 256 (with more tiles
+                               those run slot runs) */
   int gemm_tile_rows;       /* rows of one modular-GEMM output tile: 256, or 128 when
-                               128-row tiles cover M with less padding too */
+                               128-row tiles cover M with less padding too, or for
+                               shallow products of at most 40 tiles of 256 x 256 (not
+                               row-chunked) */
   int gemm_run;             /* residue slots one modular-GEMM work group runs back to back
                                for its tile; 1 (one slot per group) except for shallow
-                               products on 256 x 256 tiles (at most 32 k-steps, no
-                               K-split), whose nprimes slots split over ceil(256 / T)
-                               runs per tile when the T output tiles are fewer than
-                               256, one run when T is a multiple of 256 and three runs
-                               otherwise (1 when that leaves runs of one) */
+                               products (at most 32 k-steps, no K-split) on 256 x 256
+                               tiles, of which they have T >= 256 (fewer take 256 x 128
+                               or 128 x 128 tiles): one run of all nprimes slots when T
+                               is a multiple of 256, three runs otherwise (1 when that
+                               leaves runs of one) */
   int64_t ext_rowsA;        /* rows of each A plane (per member, per row chunk) that the
                                extraction writes: the operand rows and the zero padding
                                that GEMM tiles read (a multiple of 128, at most the padded

@@ -129,9 +129,12 @@ def test_layout_choices_fuzz():
         assert L.ksplit in (1, 2, 4, 8, 16), case
         assert L.ksplit == 1 or (L.Kp // 64) // L.ksplit >= 8, case
         assert 1 <= L.gemm_run <= max(P, 1), case
+        tiles = batch * (L.Mp // 256) * (L.Np // 256)
         if L.gemm_run > 1:
             assert (L.gemm_tile_rows, L.gemm_tile_cols, L.ksplit, L.deep) == (256, 256, 1, 0), case
-            assert L.Kp // 64 <= 32 and P >= 2, case
+            assert L.Kp // 64 <= 32 and P >= 2 and tiles >= 256, case
+        if not L.deep and L.ksplit == 1 and P >= 2 and L.Kp // 64 <= 32 and 0 < tiles < 256:
+            assert L.gemm_tile_cols == 128, case
         assert (L.gemm_tile_rows, L.gemm_tile_cols) in ((256, 256), (256, 128), (128, 128)), case
         assert capi.workspace_size_min(batch, M, N, K, P, corr) <= L.total, case
 
@@ -300,27 +303,35 @@ def test_minimum_workspace(shape):
 
 def test_slot_runs_only_for_shallow_products():
     """Runs are chosen from the shapes alone: shallow products without a
-    K-split on 256 x 256 tiles, split into ceil(256 / tiles) runs per tile
-    below 256 output tiles, one run at whole multiples of 256 tiles, three
-    runs otherwise; deep, K-split, mixed-tile, 256 x 128 or 128 x 128 tile and
-    very few-tile launches keep one slot per group."""
+    K-split with at least 256 output tiles of 256 x 256, one run at whole
+    multiples of 256 tiles, three runs otherwise; deep, K-split, mixed-tile
+    and one-modulus launches keep one slot per group, and shallow products
+    with fewer tiles run one slot per group on 256 x 128 tiles (128 x 128 at
+    40 tiles or fewer)."""
     assert capi.layout(64, 512, 512, 512, 14, True).gemm_run == 14        # c4: 256 tiles
     assert capi.layout(1, 8192, 8192, 8192, 14, True).gemm_run == 1       # c2: 128 k-steps
     assert capi.layout(1, 128, 128, 4096, 14, True).gemm_run == 1         # c1: K-split
     assert capi.layout(1, 300, 1290, 200, 14, True).gemm_run == 1         # mixed tiles
     assert capi.layout(1, 500, 500, 1024, 1, True).gemm_run == 1          # one modulus
-    assert capi.layout(32, 500, 500, 128, 14, True).gemm_run == 7         # 128 tiles: 2 runs
-    assert capi.layout(1, 2560, 2560, 200, 13, False).gemm_run == 5       # 100 tiles: 3 runs
-    # 256 x 128 and 128 x 128 tiles (two groups per CU) keep one slot per group
-    assert capi.layout(128, 40, 40, 256, 14, True).gemm_run == 1
-    assert capi.layout(64, 512, 300, 1000, 14, True).gemm_run == 1
-    assert capi.layout(64, 256, 256, 256, 14, True).gemm_run == 4         # 64 tiles: 4 runs
-    assert capi.layout(40, 256, 256, 320, 20, True).gemm_run == 3         # 40 tiles: 7 runs
-    assert capi.layout(8, 512, 512, 512, 14, True).gemm_run == 2          # 32 tiles: 8 runs
-    assert capi.layout(16, 256, 256, 256, 14, True).gemm_run == 1         # 16 tiles: runs of one
     assert capi.layout(128, 512, 512, 512, 14, True).gemm_run == 14       # 512 tiles: whole rounds
     assert capi.layout(80, 512, 512, 512, 14, True).gemm_run == 5         # 320 tiles: 3 runs
     assert capi.layout(300, 256, 256, 256, 20, True).gemm_run == 7        # 300 tiles: 3 runs
+    assert capi.layout(1, 4096, 4096, 1024, 14, True).gemm_run == 14      # 256 tiles, 16 k-steps
+    assert capi.layout(1, 4096, 4096, 4096, 14, True).gemm_run == 1       # 64 k-steps
+    # fewer than 256 tiles: one slot per group on narrow tiles
+    for shape, tile in [((32, 500, 500, 128, 14, True), (256, 128)),      # 128 tiles
+                        ((1, 2560, 2560, 200, 13, False), (256, 128)),    # 100 tiles
+                        ((64, 256, 256, 256, 14, True), (256, 128)),      # 64 tiles
+                        ((48, 512, 512, 512, 14, True), (256, 128)),      # 192 tiles
+                        ((1, 2048, 2048, 2048, 14, True), (256, 128)),    # 64 tiles, 32 k-steps
+                        ((40, 256, 256, 320, 20, True), (128, 128)),      # 40 tiles
+                        ((8, 512, 512, 512, 14, True), (128, 128)),       # 32 tiles
+                        ((16, 256, 256, 256, 14, True), (128, 128)),      # 16 tiles
+                        ((1, 1500, 1500, 1500, 14, True), (128, 128)),    # 36 tiles
+                        ((128, 40, 40, 256, 14, True), (128, 128)),
+                        ((64, 512, 300, 1000, 14, True), (256, 128))]:
+        L = capi.layout(*shape)
+        assert (L.gemm_run, L.gemm_tile_rows, L.gemm_tile_cols) == (1,) + tile, shape
 
 
 def test_sweep_reaches_every_gemm_form():
@@ -338,3 +349,19 @@ def test_sweep_reaches_every_gemm_form():
               ("tile", 128, 128, False), ("ksplit", True), ("ksplit", False), ("run", True),
               ("run", False)]:
         assert f in forms, f
+
+
+def test_run_checks_operand_extents():
+    """The C entry points read every extent from their arguments: the
+    ctypes helper refuses operands whose shapes disagree before any call."""
+    A = torch.zeros(2, 3, 5, dtype=torch.float64)
+    with pytest.raises(ValueError, match="K of A"):
+        capi.run("bmm", A, torch.zeros(2, 5, 3, dtype=torch.float64), capi_primes(3))
+    with pytest.raises(ValueError, match="batch"):
+        capi.run("bmm_nt", A, torch.zeros(3, 5, 4, dtype=torch.float64), capi_primes(3))
+    with pytest.raises(ValueError, match="K of A"):
+        capi.run("mm_nt", A[0], torch.zeros(4, 5, dtype=torch.float64), capi_primes(3))
+    with pytest.raises(ValueError, match="dims"):
+        capi.run("mm", A, torch.zeros(4, 5, dtype=torch.float64), capi_primes(3))
+    with pytest.raises(ValueError, match="contiguous float64"):
+        capi.run("mm", A[0], torch.zeros(4, 5, dtype=torch.float32), capi_primes(3))

@@ -361,33 +361,61 @@ def test_slot_run_parity(dev, kind, batch, M, N, K, primes, corr, tile):
 
 
 
-SPLIT_RUN_CASES = [
-    # kind, batch, M, N, K, moduli, corr, (tile rows, cols), expected slots per run.
-    # Fewer than 256 output tiles: each tile's slots split into ceil(256 / tiles)
-    # runs, the last one shorter; past 256 tiles and off whole rounds, three runs.
-    ("mm_nt", 1, 1792, 2560, 256, O.PRIMES[:14], True, (256, 256), 4),  # 70 tiles: 4, 4, 4, 2
-    ("mm", 1, 2560, 2560, 200, O.PRIMES[:13], False, (256, 256), 5),    # 100 tiles: 5, 5, 3
-    ("mm_nt", 1, 1280, 2048, 320, O.PRIMES[:20], True, (256, 256), 3),  # 40 tiles: six of 3, then 2
-    ("bmm", 8, 300, 400, 256, O.PRIMES[:14], True, (256, 256), 2),      # 32 tiles: seven of 2
-    ("bmm_nt", 32, 500, 500, 128, O.PRIMES[:14], True, (256, 256), 7),  # 128 tiles: 7, 7
-    ("bmm", 90, 240, 250, 192, MODULI_ORDERS[1], True, (256, 256), 5),  # 5, 5, 4; even modulus 254
-    ("bmm", 20, 240, 240, 1800, O.PRIMES[:14], True, (256, 256), 2),    # 29 k-steps per slot
-    ("bmm_nt", 300, 240, 250, 64, O.PRIMES[:14], True, (256, 256), 5),  # 300 tiles: three runs
+THREE_RUN_CASES = [
+    # kind, batch, M, N, K, moduli, corr, expected slots per run.
+    # Past 256 output tiles of 256 x 256 and off whole rounds of CUs: each tile's slots
+    # split into three runs, the last one shorter.
+    ("bmm_nt", 300, 240, 250, 64, O.PRIMES[:14], True, 5),             # 300 tiles: 5, 5, 4
+    ("bmm", 270, 250, 250, 100, MODULI_ORDERS[1], True, 5),            # even modulus 254
+    ("mm", 1, 4352, 4352, 100, O.PRIMES[:13], False, 5),               # 289 tiles: 5, 5, 3
+    ("mm_nt", 1, 4200, 4500, 120, O.PRIMES[:20], True, 7),             # 306 tiles: 7, 7, 6
 ]
 
 
-@pytest.mark.parametrize("kind,batch,M,N,K,primes,corr,tile,run", SPLIT_RUN_CASES)
-def test_split_slot_run_parity(dev, kind, batch, M, N, K, primes, corr, tile, run):
+@pytest.mark.parametrize("kind,batch,M,N,K,primes,corr,run", THREE_RUN_CASES)
+def test_split_slot_run_parity(dev, kind, batch, M, N, K, primes, corr, run):
     """Shallow products whose output tiles do not fill whole rounds of CUs:
-    each tile's residue slots split over several run groups (every group
+    each tile's residue slots split over three run groups (every group
     starts its own operand stream at its run's first plane): every stage
     against the oracle."""
     from fp64_emu import capi
     P = len(primes)
     print(f"case split slot runs {kind} b={batch} {M}x{N}x{K} P={P} corr={corr} run={run}", flush=True)
     L = capi.layout(batch, M, N, K, P, corr)
-    assert (L.gemm_run, L.ksplit) == (run, 1)
-    assert (L.gemm_tile_rows, L.gemm_tile_cols) == tile
+    assert (L.gemm_run, L.ksplit, L.gemm_tile_rows, L.gemm_tile_cols) == (run, 1, 256, 256)
+    seed = 2700 + batch + M + N + K + P
+    if kind in ("bmm", "bmm_nt"):
+        A = _randn((batch, M, K), seed, dev)
+        B = _randn((batch, K, N) if kind == "bmm_nt" else (batch, N, K), seed + 1, dev)
+    else:
+        A = _randn((M, K), seed, dev)
+        B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
+    check_call(kind, A, B, primes, use_corr=corr)
+
+
+FEW_TILE_CASES = [
+    # kind, batch, M, N, K, moduli, corr, (tile rows, cols).
+    # Shallow products of fewer than 256 output tiles of 256 x 256: one slot per group on
+    # 256 x 128 tiles, on 128 x 128 tiles at 40 tiles or fewer.
+    ("mm_nt", 1, 1792, 2560, 256, O.PRIMES[:14], True, (256, 128)),    # 70 tiles
+    ("mm", 1, 2560, 2560, 200, O.PRIMES[:13], False, (256, 128)),      # 100 tiles
+    ("mm_nt", 1, 1280, 2048, 320, O.PRIMES[:20], True, (128, 128)),    # 40 tiles
+    ("bmm", 8, 300, 400, 256, O.PRIMES[:14], True, (128, 128)),        # 32 tiles
+    ("bmm_nt", 32, 500, 500, 128, O.PRIMES[:14], True, (256, 128)),    # 128 tiles
+    ("bmm", 90, 240, 250, 192, MODULI_ORDERS[1], True, (256, 128)),    # even modulus 254
+    ("bmm", 20, 240, 240, 1800, O.PRIMES[:14], True, (128, 128)),      # 29 k-steps per slot
+]
+
+
+@pytest.mark.parametrize("kind,batch,M,N,K,primes,corr,tile", FEW_TILE_CASES)
+def test_few_tile_parity(dev, kind, batch, M, N, K, primes, corr, tile):
+    """Shallow products with fewer output tiles than CUs run one residue slot
+    per work group on the narrow launches: every stage against the oracle."""
+    from fp64_emu import capi
+    P = len(primes)
+    print(f"case few tiles {kind} b={batch} {M}x{N}x{K} P={P} corr={corr} tile={tile}", flush=True)
+    L = capi.layout(batch, M, N, K, P, corr)
+    assert (L.gemm_run, L.ksplit, L.gemm_tile_rows, L.gemm_tile_cols) == (1, 1) + tile
     seed = 2700 + batch + M + N + K + P
     if kind in ("bmm", "bmm_nt"):
         A = _randn((batch, M, K), seed, dev)

@@ -2,7 +2,7 @@
 path against the CPU oracle (through the C ABI, on a pattern-filled
 workspace), for kinds, batch counts, ragged M / N / K, modulus counts,
 correction on and off and both combines drawn from a fixed generator.  The
-draws, with a few shallow ones on 256 x 256 tiles, reach every GEMM launch form
+draws, with a few shallow ones of 256 and more 256 x 256 tiles, reach every GEMM launch form
 (256 x 256, 256 x 128, 128 x 128 and mixed tiles; K-splits; slot runs), as a
 CPU-tier test of the draws checks.
 A second sweep draws the reference accuracy study's input distributions
@@ -41,10 +41,12 @@ CASES = _cases()
 def _run_cases():
     """Shallow products on 256 x 256 output tiles, the launches that run each
     tile's residue slots back to back: batched members of one tile each
-    (130..290 members: two runs per tile below 256 tiles, one at 256, three
-    above), and single products of 16..18 tile rows and columns (columns whose
-    last tile holds more than 128 of them, so that no mixed launch takes
-    them); ragged K, modulus counts, correction on and off."""
+    (256..290 members: one run per tile at 256 tiles, three above), and
+    single products of 16..18 tile rows and columns (columns whose last tile
+    holds more than 128 of them, so that no mixed launch takes them); ragged
+    K, modulus counts, correction on and off.  Then one shallow product of as
+    many tiles whose last tile column holds at most 128 columns: the mixed
+    launch, one slot per group."""
     rng = np.random.default_rng(20261205)
     out = []
     for i in range(6):
@@ -53,7 +55,7 @@ def _run_cases():
         exact = bool(rng.integers(4))
         if i % 2 == 0:
             kind = ["bmm", "bmm_nt"][rng.integers(2)]
-            batch = int(rng.choice([int(rng.integers(130, 256)), 256, int(rng.integers(257, 291))]))
+            batch = int(rng.choice([int(rng.integers(257, 291)), 256, int(rng.integers(257, 291))]))
             M = int(rng.integers(233, 257))
             N = int(rng.integers(233, 257))
             K = int(rng.integers(1, 131))
@@ -64,6 +66,10 @@ def _run_cases():
             N = 256 * int(rng.integers(16, 19)) - int(rng.integers(0, 128))
             K = int(rng.integers(1, 121))
         out.append((100 + i, kind, batch, M, N, K, P, corr, exact))
+    M = 256 * int(rng.integers(16, 19)) - int(rng.integers(0, 128))
+    N = 256 * int(rng.integers(16, 19)) - int(rng.integers(128, 256))
+    out.append((106, ["mm", "mm_nt"][rng.integers(2)], 1, M, N, int(rng.integers(1, 121)),
+                int(rng.integers(3, 21)), bool(rng.integers(2)), True))
     return out
 
 
