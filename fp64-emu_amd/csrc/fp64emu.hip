@@ -482,48 +482,54 @@ __device__ __forceinline__ void row_pass(const double* __restrict__ x, int64_t c
 }
 
 // kGroup: few rows (not enough waves to fill the chip): a 256-thread group
-// per row, wave w running sum 64 w + l alone (sixteen of its loads in
-// flight), the four waves' sums meeting in LDS before the same fold.
-template <bool kGroup>
+// per row, its wave w running sum 64 w + l alone (sixteen of its loads in
+// flight), the four waves' sums meeting in LDS before the same fold.  A
+// block of kWaves waves holds kWaves / 4 such groups, or kWaves rows (one
+// per wave) otherwise.
+template <bool kGroup, int kWaves>
 __device__ __forceinline__ void size_rows_body(int64_t bid, const double* __restrict__ A, int64_t rowsA,
                                                const double* __restrict__ B, int64_t rows, int64_t K,
                                                int bits, int16_t* __restrict__ sftA,
                                                float* __restrict__ lgA, int16_t* __restrict__ sftB,
                                                float* __restrict__ lgB) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t row = kGroup ? bid : bid * kRowsPerBlock + wave;
-  if (row >= rows) return;
+  const int64_t row = kGroup ? bid * (kWaves / 4) + (wave >> 2) : bid * kWaves + wave;
   const bool isA = row < rowsA;
   const int64_t r = isA ? row : row - rowsA;
   const double* __restrict__ x = (isA ? A : B) + r * K + lane;
   double mx = 0.0, ss[4] = {0.0, 0.0, 0.0, 0.0};
   if constexpr (kGroup) {
-    const double* __restrict__ xw = x + 64 * wave;
+    // Every wave reaches the barrier; rows past the last only skip loads.
+    const int wg = wave & 3;
+    const double* __restrict__ xw = x + 64 * wg;
     double sw = 0.0, mw = 0.0;
     // Elements past K read as 0, which leaves both the max and the sum
     // (never -0) unchanged.
-    for (int64_t c = 0; c < K; c += 4096) {
-      double v[16];
+    if (row < rows) {
+      for (int64_t c = 0; c < K; c += 4096) {
+        double v[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        v[i] = c + 256 * i + 64 * wave + lane < K ? xw[c + 256 * i] : 0.0;
+        for (int i = 0; i < 16; ++i)
+          v[i] = c + 256 * i + 64 * wg + lane < K ? xw[c + 256 * i] : 0.0;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        mw = fmax(mw, fabs(v[i]));
-        sw = fma(v[i], v[i], sw);
+        for (int i = 0; i < 16; ++i) {
+          mw = fmax(mw, fabs(v[i]));
+          sw = fma(v[i], v[i], sw);
+        }
       }
     }
-    __shared__ double sh_ss[4][64], sh_mx[4][64];
+    __shared__ double sh_ss[kWaves][64], sh_mx[kWaves][64];
     sh_ss[wave][lane] = sw;
     sh_mx[wave][lane] = mw;
     __syncthreads();
-    if (wave != 0) return;
+    if (wg != 0 || row >= rows) return;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      ss[u] = sh_ss[u][lane];
-      mx = fmax(mx, sh_mx[u][lane]);
+      ss[u] = sh_ss[wave + u][lane];
+      mx = fmax(mx, sh_mx[wave + u][lane]);
     }
   } else {
+    if (row >= rows) return;
     // Sixteen loads in flight, then eight, then guarded 256-element blocks.
     int64_t c = 0;
     for (; c + 1024 <= K; c += 1024) row_pass<4>(x, c, mx, ss);
@@ -559,7 +565,7 @@ __global__ void __launch_bounds__(kThreads)
 size_rows_kernel(const double* __restrict__ A, int64_t rowsA, const double* __restrict__ B,
                  int64_t rows, int64_t K, int bits, int16_t* __restrict__ sftA,
                  float* __restrict__ lgA, int16_t* __restrict__ sftB, float* __restrict__ lgB) {
-  size_rows_body<kGroup>(blockIdx.x, A, rowsA, B, rows, K, bits, sftA, lgA, sftB, lgB);
+  size_rows_body<kGroup, kThreads / 64>(blockIdx.x, A, rowsA, B, rows, K, bits, sftA, lgA, sftB, lgB);
 }
 
 // A wave per row when the rows give the chip at least four waves per SIMD,
@@ -574,6 +580,100 @@ void launch_size_rows(int64_t rows, hipStream_t s, const double* A, int64_t rows
   else
     hipLaunchKernelGGL(size_rows_kernel<false>, dim3((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock)),
                        dim3(kThreads), 0, s, A, rowsA, B, rows, K, bits, sftA, lgA, sftB, lgB);
+}
+
+// The sizing of A's rows and of the [K, N] operand's columns in one launch
+// of 1024-thread groups.  Column statistics follow fp64_emu_cuda/fp64_emu.cu:148-189,
+// which takes them in two launches (slab partials, then their fold): per
+// column, nslab k-slabs of kslab rows (slab_split), each slab's max |x| and
+// FMA-accumulated sum of squares taken over its rows in order, then folded
+// in slab order.  Here a column group holds cpw = 1024 / nslab columns and
+// every slab of each: thread t takes slab t / cpw of column t % cpw (adjacent
+// threads read adjacent columns of one operand row), its partials meet in
+// LDS, and one thread per column folds them, so no partials go through
+// memory and no second launch waits for them.  The column groups come
+// first: each thread walks its slab's rows in one dependent chain, so they
+// are the launch's longest groups, and starting them first lets the row
+// groups (16 rows per group, a wave each; 4 rows of 256 threads when the
+// rows are few) fill in around them.
+// For slabs of at most kFusedSlabRows rows.  Past that the ~128 column
+// groups (nslab x columns is about 131072 from 1024 columns on) hold long
+// chains on half the CUs, and the two-launch form, whose slab groups spread
+// over every CU, measured faster (1023 x 2049 x 32769: 1.62 against 1.66 ms
+// per call; 100 x 20000 x 3000: 0.673 against 0.704 ms); at 128-row slabs
+// the single launch was even or faster (batched 64 x 512^3 0.497 -> 0.485
+// ms, 4096^3 even), and on small products it saves the second launch
+// (128 x 128 x 4096 48.3 -> 46.2 us, 512^3 43.5 -> 38.8 us, 1000^3 70.9 ->
+// 66.3 us).
+constexpr int kSizeThreads = 1024;
+constexpr int64_t kFusedSlabRows = 256;
+
+template <bool kGroup>
+__global__ void __launch_bounds__(kSizeThreads)
+size_rows_cols_kernel(const double* __restrict__ A, int64_t rowsA, int64_t ncolgrp, int64_t K, int bits,
+                      int16_t* __restrict__ sftA, float* __restrict__ lgA,
+                      const double* __restrict__ X, int64_t totalcols, int64_t cols_per,
+                      int64_t kslab, int nslab, int cpw, int16_t* __restrict__ sftB,
+                      float* __restrict__ lgB) {
+  const int64_t bid = blockIdx.x;
+  if (bid >= ncolgrp) {
+    size_rows_body<kGroup, kSizeThreads / 64>(bid - ncolgrp, A, rowsA, A, rowsA, K, bits, sftA, lgA,
+                                              nullptr, nullptr);
+    return;
+  }
+  __shared__ double sh_m[kSizeThreads], sh_s[kSizeThreads];
+  const int t = threadIdx.x;
+  const int sl = t / cpw, c = t - sl * cpw;
+  const int64_t j = bid * cpw + c;
+  double mx = 0.0, ss = 0.0;
+  if (sl < nslab && j < totalcols) {
+    const int64_t b = j / cols_per, n = j - b * cols_per;
+    const int64_t k0 = (int64_t)sl * kslab;
+    const int64_t k1 = min(k0 + kslab, K);
+    const double* __restrict__ base = X + b * K * cols_per + n;
+    // Sixteen rows in flight per thread; the fma chain keeps the slab order.
+    int64_t k = k0;
+    for (; k + 16 <= k1; k += 16) {
+      double v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = base[(k + u) * cols_per];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        mx = fmax(mx, fabs(v[u]));
+        ss = fma(v[u], v[u], ss);
+      }
+    }
+    for (; k < k1; ++k) {
+      const double v = base[k * cols_per];
+      mx = fmax(mx, fabs(v));
+      ss = fma(v, v, ss);
+    }
+  }
+  sh_m[t] = mx;
+  sh_s[t] = ss;
+  __syncthreads();
+  if (t >= cpw || j >= totalcols) return;
+  // Slabs folded in order, sixteen LDS reads ahead of the adds.
+  double fm = 0.0, fs = 0.0;
+  int q = 0;
+  for (; q + 16 <= nslab; q += 16) {
+    double m[16], v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      m[u] = sh_m[(q + u) * cpw + t];
+      v[u] = sh_s[(q + u) * cpw + t];
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      fm = fmax(fm, m[u]);
+      fs = fs + v[u];
+    }
+  }
+  for (; q < nslab; ++q) {
+    fm = fmax(fm, sh_m[q * cpw + t]);
+    fs = fs + sh_s[q * cpw + t];
+  }
+  row_stats_out(fm, fs, bits, &sftB[j], &lgB[j]);
 }
 
 // Column partials of a [K, N] operand (per batch member): thread j owns
@@ -612,24 +712,27 @@ __device__ __forceinline__ void size_cols_partial_body(int64_t bx, int64_t by, c
   pss[by * totalcols + j] = ss;
 }
 
-// The sizing of A's rows and of the [K, N] operand's column slabs in one
-// launch: groups [0, ncol) take column slabs (x fastest), the rest rows.
+// Deep columns (slabs of more than kFusedSlabRows rows): the sizing of A's
+// rows and of the [K, N] operand's column slabs in one launch of 256-thread
+// groups, groups [0, ncol) taking column slabs (x fastest), the rest rows;
+// size_cols_final_kernel then folds the slabs.
 // The slab groups come first: each thread walks its slab's rows in one
 // dependent chain, so they are the launch's longest groups, and starting
 // them first lets the row groups fill in around them instead of leaving
 // them as a tail.
 template <bool kGroup>
 __global__ void __launch_bounds__(kThreads)
-size_rows_cols_kernel(const double* __restrict__ A, int64_t rowsA, int64_t ncol, int64_t K, int bits,
-                      int16_t* __restrict__ sftA, float* __restrict__ lgA,
-                      const double* __restrict__ X, int64_t totalcols, int64_t cols_per,
-                      int64_t kslab, int64_t gcx, double* __restrict__ pmax,
-                      double* __restrict__ pss) {
+size_rows_slabs_kernel(const double* __restrict__ A, int64_t rowsA, int64_t ncol, int64_t K, int bits,
+                       int16_t* __restrict__ sftA, float* __restrict__ lgA,
+                       const double* __restrict__ X, int64_t totalcols, int64_t cols_per,
+                       int64_t kslab, int64_t gcx, double* __restrict__ pmax,
+                       double* __restrict__ pss) {
   const int64_t bid = blockIdx.x;
   if (bid < ncol) {
     size_cols_partial_body(bid % gcx, bid / gcx, X, totalcols, K, cols_per, kslab, pmax, pss);
   } else {
-    size_rows_body<kGroup>(bid - ncol, A, rowsA, A, rowsA, K, bits, sftA, lgA, nullptr, nullptr);
+    size_rows_body<kGroup, kThreads / 64>(bid - ncol, A, rowsA, A, rowsA, K, bits, sftA, lgA, nullptr,
+                                          nullptr);
   }
 }
 
@@ -700,10 +803,10 @@ constexpr int kPickThreads = 1024;
 
 __device__ __forceinline__ float max4(float4 v) { return fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)); }
 
-// Max of lg[0, n) in one block: eight float4 loads in flight per thread
-// (the workspace slices are 256-byte aligned), a scalar tail.
+// Max of lg[0, n) over a block of T threads: eight float4 loads in flight
+// per thread (the workspace slices are 256-byte aligned), a scalar tail.
+template <int T>
 __device__ __forceinline__ float block_max_lg(const float* __restrict__ lg, int64_t n, int tid) {
-  constexpr int T = kPickThreads;
   const float4* __restrict__ v4 = reinterpret_cast<const float4*>(lg);
   const int64_t n4 = n / 4;
   float a = -INFINITY;
@@ -720,39 +823,68 @@ __device__ __forceinline__ float block_max_lg(const float* __restrict__ lg, int6
   return a;
 }
 
-__global__ void __launch_bounds__(kPickThreads)
-pick_width_kernel(const float* __restrict__ lgA, int64_t m, const float* __restrict__ lgB,
-                  int64_t n, float log2M, int bits, int* __restrict__ bits_eff) {
-  constexpr int T = kPickThreads;
+// max lgA[0, m) and max lgB[0, n), in every thread of a block of T (the
+// values are +-inf or finite, so the order of the maxima does not matter).
+template <int T>
+__device__ __forceinline__ void block_max_lg_pair(const float* __restrict__ lgA, int64_t m,
+                                                  const float* __restrict__ lgB, int64_t n, float& a,
+                                                  float& b) {
   __shared__ float sa[T / 64], sb[T / 64];
   const int tid = threadIdx.x;
-  float a = block_max_lg(lgA, m, tid);
-  float b = block_max_lg(lgB, n, tid);
+  a = block_max_lg<T>(lgA, m, tid);
+  b = block_max_lg<T>(lgB, n, tid);
 #pragma unroll
   for (int s = 32; s > 0; s >>= 1) {
-    a = fmaxf(a, __shfl_down(a, s));
-    b = fmaxf(b, __shfl_down(b, s));
+    a = fmaxf(a, __shfl_xor(a, s));
+    b = fmaxf(b, __shfl_xor(b, s));
   }
   if ((tid & 63) == 0) {
     sa[tid >> 6] = a;
     sb[tid >> 6] = b;
   }
   __syncthreads();
-  if (tid == 0) {
+  a = sa[0];
+  b = sb[0];
 #pragma unroll
-    for (int w = 1; w < T / 64; ++w) {
-      a = fmaxf(a, sa[w]);
-      b = fmaxf(b, sb[w]);
-    }
-    const float need = a + b + 0.5f;
-    int g = 0;
-    if (isfinite(need)) g = (int)floorf((log2M - 1.0f - need) * 0.5f);
-    g = min(g, 53 - bits);
-    const int be = max(bits + g, 16);
+  for (int w = 1; w < T / 64; ++w) {
+    a = fmaxf(a, sa[w]);
+    b = fmaxf(b, sb[w]);
+  }
+}
+
+// be from the maxima of the row and column log2-norms.
+__device__ __forceinline__ int pick_width(float a, float b, float log2M, int bits) {
+  const float need = a + b + 0.5f;
+  int g = 0;
+  if (isfinite(need)) g = (int)floorf((log2M - 1.0f - need) * 0.5f);
+  g = min(g, 53 - bits);
+  return max(bits + g, 16);
+}
+
+__global__ void __launch_bounds__(kPickThreads)
+pick_width_kernel(const float* __restrict__ lgA, int64_t m, const float* __restrict__ lgB,
+                  int64_t n, float log2M, int bits, int* __restrict__ bits_eff) {
+  float a, b;
+  block_max_lg_pair<kPickThreads>(lgA, m, lgB, n, a, b);
+  if (threadIdx.x == 0) {
+    const int be = pick_width(a, b, log2M, bits);
     bits_eff[0] = be;
     bits_eff[1] = be - bits;
   }
 }
+
+// Products of at most kPickInExtractMax rows and columns in all (one row
+// chunk, one K segment) take the width pick inside the extraction instead:
+// every extraction group reads both log2-norm vectors (at most 16 KiB) and
+// reduces them itself, and group 0 stores bits_eff for the reconstruction,
+// which saves the pick's launch (small products are bound by their chain of
+// launches).  Measured against the separate launch: 512^3 mm_nt 43.5 ->
+// 37.8 us with the single column-sizing launch, mm 36.9 -> 35.3 us, 1000^3
+// 64.7 -> 62.6 us (mm); up to kPickInExtractBytes of those reads over the
+// launch (2048^3: 32 MiB, still 3% faster); past it the reads cost more
+// than the launch (1023 x 2049 x 32769: 295 MiB, 1.609 against 1.620 ms).
+constexpr int64_t kPickInExtractMax = 4096;
+constexpr int64_t kPickInExtractBytes = 64ll << 20;
 
 // ---------------------------------------------------------------------------
 // Extraction.  Element semantics follow fp64_emu_cuda/fp64_emu.cu:288-321
@@ -818,6 +950,14 @@ struct ExtractArgs {
   const int16_t* sftA;
   const int16_t* sftB;
   const int* bits_eff;
+  // pick != 0: the width pick from lgA[0, nlgA) and lgB[0, nlgB) in every
+  // group; group 0 stores bits_eff (bits_out) for the reconstruction.
+  int pick, bits;
+  float log2M;
+  const float* lgA;
+  const float* lgB;
+  int64_t nlgA, nlgB;
+  int* bits_out;
   int8_t* planesA;
   int8_t* planesB;
   ModTables tab;
@@ -830,6 +970,18 @@ template <bool kDefault>
 __global__ void __launch_bounds__(kThreads)
 extract_kernel(ExtractArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The width pick, when this launch takes it: every wave reaches the
+  // block's barrier before any returns.
+  int pick_be = 0;
+  if (a.pick) {
+    float ma, mb;
+    block_max_lg_pair<kThreads>(a.lgA, a.nlgA, a.lgB, a.nlgB, ma, mb);
+    pick_be = pick_width(ma, mb, a.log2M, a.bits);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      a.bits_out[0] = pick_be;
+      a.bits_out[1] = pick_be - a.bits;
+    }
+  }
   // Work groups: the row groups holding operand rows of A, then of B, then
   // the all-padding row groups of A and of B (zero stores only), so that the
   // work spreads evenly over the XCDs (group i runs on XCD i % 8) whatever
@@ -921,8 +1073,8 @@ extract_kernel(ExtractArgs a) {
   // Shift: per row of A / of B [N,K]; per column of B [K,N] -- one per lane.
   // Read after the operand loads are issued, so one round trip covers both.
   const int16_t* sfts = isA ? a.sftA : a.sftB;
-  const int be = a.bits_eff[0];
-  const int shift = rowok ? (int)sfts[b * R + r] + a.bits_eff[1] : 0;
+  const int be = a.pick ? pick_be : a.bits_eff[0];
+  const int shift = rowok ? (int)sfts[b * R + r] + (a.pick ? pick_be - a.bits : a.bits_eff[1]) : 0;
 
   // Split every element first: th, tl as exact doubles, hi7/q7 bytes.  All
   // scalings are by powers of two and exact: y = |x| 2^shift (< 2^be, or
@@ -2445,10 +2597,15 @@ int run(const Call& c) {
     const int64_t limit = (int64_t)0xFFFFFFFFu / kThreads;
     int64_t kslab; int nslab;
     slab_split(NF, c.K, &kslab, &nslab);
-    const int64_t sizing = !c.b_kn ? (MF + NF < kRowsGroupBelow ? MF + NF
-                                                                 : (MF + NF + kRowsPerBlock - 1) / kRowsPerBlock)
-                                   : (MF < kRowsGroupBelow ? MF : (MF + kRowsPerBlock - 1) / kRowsPerBlock) +
-                                         (NF + kThreads - 1) / kThreads * nslab;
+    // (In groups of kThreads; the single column-sizing launch's groups are
+    // kSizeThreads wide.)
+    const bool group = MF < kRowsGroupBelow;
+    const int64_t sizing =
+        !c.b_kn ? (MF + NF < kRowsGroupBelow ? MF + NF : (MF + NF + kRowsPerBlock - 1) / kRowsPerBlock)
+        : kslab <= kFusedSlabRows
+            ? ((group ? (MF + 3) / 4 : (MF + 15) / 16) +
+               (NF + kSizeThreads / nslab - 1) / (kSizeThreads / nslab)) * (kSizeThreads / kThreads)
+            : (group ? MF : (MF + kRowsPerBlock - 1) / kRowsPerBlock) + (NF + kThreads - 1) / kThreads * nslab;
     const int64_t extraction = c.batch * (L.ext_rowsA / 64 + L.ext_rowsB / 64) * (L.Kp / kTileK);
     const int64_t recon = c.batch * ((std::min<int64_t>(L.chunk_rows, c.M) + 15) / 16) * ((c.N + 63) / 64);
     for (int64_t gsz : {sizing, extraction, ga.total, recon})
@@ -2461,23 +2618,42 @@ int run(const Call& c) {
   } else {
     int64_t kslab; int nslab;
     slab_split(NF, c.K, &kslab, &nslab);
-    const int64_t gcx = (NF + kThreads - 1) / kThreads;
-    // K > 0 here, so nslab >= 1.
     const bool group = MF < kRowsGroupBelow;
-    const int64_t nrow = group ? MF : (MF + kRowsPerBlock - 1) / kRowsPerBlock;
-    const unsigned grid = (unsigned)(nrow + gcx * nslab);
-    const int64_t ncol = gcx * nslab;
-    if (group)
-      hipLaunchKernelGGL(size_rows_cols_kernel<true>, dim3(grid), dim3(kThreads), 0, s, c.A, MF, ncol,
-                         c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, gcx, pmax, pss);
-    else
-      hipLaunchKernelGGL(size_rows_cols_kernel<false>, dim3(grid), dim3(kThreads), 0, s, c.A, MF, ncol,
-                         c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, gcx, pmax, pss);
-    hipLaunchKernelGGL(size_cols_final_kernel, dim3((unsigned)((NF + kFinalCols - 1) / kFinalCols)),
-                       dim3(kThreads), 0, s, pmax, pss, NF, nslab, c.bits, sftB, lgB);
+    if (kslab <= kFusedSlabRows) {
+      // K > 0 here, so 1 <= nslab <= kMaxSlab and a group holds >= 8 columns.
+      const int cpw = kSizeThreads / nslab;
+      const int64_t ncolgrp = (NF + cpw - 1) / cpw;
+      const int64_t nrow = group ? (MF + kSizeThreads / 256 - 1) / (kSizeThreads / 256)
+                                 : (MF + kSizeThreads / 64 - 1) / (kSizeThreads / 64);
+      const unsigned grid = (unsigned)(nrow + ncolgrp);
+      if (group)
+        hipLaunchKernelGGL(size_rows_cols_kernel<true>, dim3(grid), dim3(kSizeThreads), 0, s, c.A, MF,
+                           ncolgrp, c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, nslab, cpw, sftB, lgB);
+      else
+        hipLaunchKernelGGL(size_rows_cols_kernel<false>, dim3(grid), dim3(kSizeThreads), 0, s, c.A, MF,
+                           ncolgrp, c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, nslab, cpw, sftB, lgB);
+    } else {
+      const int64_t gcx = (NF + kThreads - 1) / kThreads;
+      const int64_t nrow = group ? MF : (MF + kRowsPerBlock - 1) / kRowsPerBlock;
+      const unsigned grid = (unsigned)(nrow + gcx * nslab);
+      const int64_t ncol = gcx * nslab;
+      if (group)
+        hipLaunchKernelGGL(size_rows_slabs_kernel<true>, dim3(grid), dim3(kThreads), 0, s, c.A, MF, ncol,
+                           c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, gcx, pmax, pss);
+      else
+        hipLaunchKernelGGL(size_rows_slabs_kernel<false>, dim3(grid), dim3(kThreads), 0, s, c.A, MF, ncol,
+                           c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, gcx, pmax, pss);
+      hipLaunchKernelGGL(size_cols_final_kernel, dim3((unsigned)((NF + kFinalCols - 1) / kFinalCols)),
+                         dim3(kThreads), 0, s, pmax, pss, NF, nslab, c.bits, sftB, lgB);
+    }
   }
-  hipLaunchKernelGGL(pick_width_kernel, dim3(1), dim3(kPickThreads), 0, s, lgA, MF, lgB, NF,
-                     std::min(tab.log2M, 126.0f), c.bits, bits_eff);
+  const float log2M = std::min(tab.log2M, 126.0f);
+  const int64_t ext_groups = c.batch * (L.ext_rowsA / 64 + L.ext_rowsB / 64) * (L.Kp / kTileK);
+  const bool pick_in_extract = L.nchunk == 1 && L.nseg == 1 && MF + NF <= kPickInExtractMax &&
+                               (MF + NF) * (int64_t)sizeof(float) * ext_groups <= kPickInExtractBytes;
+  if (!pick_in_extract)
+    hipLaunchKernelGGL(pick_width_kernel, dim3(1), dim3(kPickThreads), 0, s, lgA, MF, lgB, NF, log2M,
+                       c.bits, bits_eff);
 
   // 2-4. Per row chunk of A (one unless the workspace is short) and per K
   // segment (one unless deep): extraction (covering the padded planes
@@ -2508,6 +2684,8 @@ int run(const Call& c) {
       ea.div_rg[2] = make_fastdiv(ea.rgA - ea.rgA_data);
       ea.div_rg[3] = make_fastdiv(ea.rgB - ea.rgB_data);
       ea.sftA = sftA + m0; ea.sftB = sftB; ea.bits_eff = bits_eff;
+      ea.pick = pick_in_extract ? 1 : 0; ea.bits = c.bits; ea.log2M = log2M;
+      ea.lgA = lgA; ea.lgB = lgB; ea.nlgA = MF; ea.nlgB = NF; ea.bits_out = bits_eff;
       ea.planesA = planesA; ea.planesB = planesB;
       ea.tab = tab;
       const int64_t wg = c.batch * (ea.rgA + ea.rgB) * nkt;

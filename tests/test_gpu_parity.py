@@ -266,7 +266,7 @@ NARROW_CASES = [
 @pytest.mark.parametrize("kind,batch,M,N,K,primes,corr", NARROW_CASES)
 def test_narrow_tile_parity(dev, kind, batch, M, N, K, primes, corr):
     """Products whose 256-column tiles would be mostly padding run 128-column
-    tiles (two work groups per CU; shallow ones as slot runs): every stage
+    tiles (two work groups per CU, one residue slot each): every stage
     against the oracle."""
     from fp64_emu import capi
     print(f"case narrow GEMM {kind} b={batch} {M}x{N}x{K} P={len(primes)} corr={corr}", flush=True)
@@ -282,9 +282,9 @@ def test_narrow_tile_parity(dev, kind, batch, M, N, K, primes, corr):
 
 
 @pytest.mark.parametrize("kind,batch,M,N,K", [
-    ("mm", 1, 300, 1290, 200),        # last tile column: 10 of 256 columns
+    ("mm", 1, 300, 1290, 2200),       # last tile column: 10 of 256 columns
     ("mm_nt", 1, 64, 1300, 20000),    # the same under a K-split
-    ("bmm", 2, 100, 1408, 130),       # 128 of 256: the narrow half exactly full
+    ("bmm", 48, 60, 1408, 130),       # 128 of 256: the narrow half exactly full
 ])
 def test_mixed_tile_parity(dev, kind, batch, M, N, K):
     """Wide GEMM tiles whose last tile column holds at most 128 columns of N
