@@ -233,6 +233,49 @@ def test_extreme_magnitudes(dev):
     assert torch.isinf(o[:10, :9]).any() and (o[10:20, 9:18] == 0).any()
 
 
+def _slab_rows(NF, K):
+    """Rows per column slab of a [K, NF] operand (the reference's slab split)."""
+    nsl0 = min(max(131072 // NF, 1), 128)
+    return -(-K // nsl0)
+
+
+SIZING_FORM_CASES = [
+    # kind, batch, M, N, K -- the sizing form in the comment
+    ("mm_nt", 1, 8, 1024, 32768),    # slabs of 256 rows: one launch (row and column groups)
+    ("mm_nt", 1, 8, 1024, 32769),    # 257 rows: slab partials, then their fold
+    ("bmm_nt", 3, 5, 77, 700),       # 117 slabs, 8 columns per group straddling members
+    ("bmm_nt", 2, 300, 1, 2000),     # one column per member
+    ("mm_nt", 1, 4500, 40, 9),       # rows past 4096: a wave per row, 16 rows per group
+    ("mm_nt", 1, 2048, 2048, 64),    # 4096 rows and columns: the width pick in the extraction
+    ("mm_nt", 1, 2049, 2048, 64),    # 4097: the width pick's own launch
+    ("mm", 1, 1000, 3000, 100),      # rows of both operands, pick in the extraction
+]
+
+
+@pytest.mark.parametrize("kind,batch,M,N,K", SIZING_FORM_CASES)
+def test_sizing_forms(dev, kind, batch, M, N, K):
+    """Each form of the sizing (one launch for rows and shallow column slabs
+    folded in LDS, or slab partials then their fold; the width pick in its
+    own launch or inside the extraction) against the oracle, on operands
+    whose rows and columns span 2^-40 .. 2^40, so that every row and column
+    takes its own shift."""
+    from fp64_emu import capi
+    print(f"case sizing form {kind} b={batch} {M}x{N}x{K}", flush=True)
+    if kind.endswith("_nt"):
+        fused = _slab_rows(batch * N, K) <= 256
+        print(f"  column slabs of {_slab_rows(batch * N, K)} rows: {'one launch' if fused else 'two'}",
+              flush=True)
+    g = torch.Generator().manual_seed(4100 + M + N + K)
+    sa = torch.pow(2.0, torch.randint(-40, 41, (batch, M, 1), generator=g).double())
+    sb = torch.pow(2.0, torch.randint(-40, 41, (batch, 1, N), generator=g).double())
+    A = torch.randn((batch, M, K), dtype=torch.float64, generator=g) * sa
+    Bt = torch.randn((batch, K, N), dtype=torch.float64, generator=g) * sb
+    B = Bt if kind.endswith("_nt") else Bt.transpose(1, 2).contiguous()
+    if batch == 1 and not kind.startswith("bmm"):
+        A, B = A[0], B[0]
+    check_call(kind, A.to(dev), B.to(dev), O.PRIMES[:14])
+
+
 @pytest.mark.parametrize("kind,batch,M,N,K,P,exact", [
     ("bmm", 2, 40, 30, 5000, 14, True),       # K-split with batch > 1 (split-major planes)
     ("mm_nt", 1, 50, 60, 20000, 15, False),   # K-split, inexact combine
