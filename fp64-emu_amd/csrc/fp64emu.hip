@@ -2,18 +2,26 @@
 // declared in include/fp64emu.h.
 //
 // Pipeline per call (one HIP stream, no host synchronisation, no allocation):
-//   1. sizing      size_rows_kernel / size_cols_* / pick_width_kernel
-//                  per-row (A) and per-column (B) power-of-two shifts, the
-//                  Cauchy-Schwarz width pick, bits_eff kept on the device.
-//   2. extraction  extract_kernel: integer-only RNE scaling of the fp64
-//                  encoding, balanced residues for every modulus and the
+//   1. sizing      size_rows_cols_kernel (rows of A and columns of a [K, N]
+//                  B in one launch) or size_rows_slabs_kernel +
+//                  size_cols_final_kernel (deep column slabs), or
+//                  size_rows_kernel (rows of both operands); then
+//                  pick_width_kernel, or the same pick inside the
+//                  extraction for small products: per-row (A) and
+//                  per-column (B) power-of-two shifts, the Cauchy-Schwarz
+//                  width pick, bits_eff kept on the device.
+//   2. extraction  extract_kernel: exact power-of-two scaling and RNE of the
+//                  fp64 values, balanced residues for every modulus and the
 //                  hi7/q7 correction operands, written directly in the
 //                  MFMA fragment order of the GEMM (tile-blocked planes).
-//   3. modgemm     modgemm_kernel: one INT8-MFMA engine over all
-//                  (slot, batch member, 256x256 tile) work items, LDS
-//                  double-buffered, XCD-aware tile order; epilogue reduces
-//                  residue slots to balanced int8 and stores correction
-//                  slots as raw int32.
+//   3. modgemm     modgemm_kernel / modgemm_mixed_kernel: one INT8-MFMA
+//                  engine over all (slot, batch member, output tile, K
+//                  split) work items, a 4-stage LDS ring fed by direct
+//                  global-to-LDS copies, XCD-aware work order, 256 x 256,
+//                  256 x 128 or 128 x 128 tiles, residue slots of shallow
+//                  products run back to back; the epilogue reduces residue
+//                  slots to balanced int8 and stores correction slots as
+//                  raw int32.
 //   4. reconstruct reconstruct_kernel: balanced Garner digits with
 //                  v_dot4_i32_i8, grouped Horner, exact 128-bit combine with
 //                  the correction, correctly rounded conversion, rescale.
