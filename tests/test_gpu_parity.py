@@ -233,6 +233,33 @@ def test_extreme_magnitudes(dev):
     assert torch.isinf(o[:10, :9]).any() and (o[10:20, 9:18] == 0).any()
 
 
+@pytest.mark.parametrize("kind", ["mm_nt", "mm"])
+def test_int32_accumulation_bound(dev, kind):
+    """K = 131071, the deepest single launch, with every residue modulo 256
+    at -128: the p = 256 slot accumulates K * 2^14 = 2^31 - 2^14, the largest
+    sum the int32 GEMM must hold (fp64_emu.cu's K bound).  x = 1 + 2^-42 puts
+    its lowest set bit at 2^7 after the shift the plan gives (be = 50)."""
+    from parity_util import oracle_sizing
+    M = N = 16
+    K = 131071
+    print(f"case int32 bound {kind} {M}x{N}x{K}", flush=True)
+    x = 1.0 + 2.0 ** -42
+    A = torch.full((M, K), x, dtype=torch.float64)
+    Bt = torch.full((K, N), x, dtype=torch.float64)
+    A[::2] *= -1.0
+    Bt[:, ::3] *= -1.0
+    primes = O.PRIMES[:15]                      # plan_config(131071)
+    be, sA, _, _, _ = oracle_sizing(A.numpy(), Bt.numpy(), True, np.asarray(primes, np.int32), 53)
+    res = np.asarray(O.extract_operand(A.numpy()[None], 0, sA, be, np.asarray(primes, np.int32),
+                                       True)[0])
+    assert be == 50 and np.all(np.abs(res[0, 0].astype(np.int32)) == 128)
+    B = Bt if kind == "mm_nt" else Bt.t().contiguous()
+    out, _, _ = check_call(kind, A.to(dev), B.to(dev), primes)
+    sign = torch.outer(torch.tensor([-1.0 if i % 2 == 0 else 1.0 for i in range(M)], dtype=torch.float64),
+                       torch.tensor([-1.0 if j % 3 == 0 else 1.0 for j in range(N)], dtype=torch.float64))
+    assert torch.equal(out.cpu(), sign * (K * x * x))
+
+
 def _slab_rows(NF, K):
     """Rows per column slab of a [K, NF] operand (the reference's slab split)."""
     nsl0 = min(max(131072 // NF, 1), 128)
