@@ -365,3 +365,23 @@ def test_run_checks_operand_extents():
         capi.run("mm", A, torch.zeros(4, 5, dtype=torch.float64), capi_primes(3))
     with pytest.raises(ValueError, match="contiguous float64"):
         capi.run("mm", A[0], torch.zeros(4, 5, dtype=torch.float32), capi_primes(3))
+
+
+def test_baseline_config_launch_forms():
+    """The launch forms of the BASELINE configs, which the profiles and the
+    bench figures were measured with (K-split, GEMM tile, slot run, correction
+    planes, sizing slabs): a layout change that moves one of them is a
+    deliberate one."""
+    forms = {
+        "c1": ((1, 128, 128, 4096, 14, True), (8, 128, 128, 1, 2, 128)),
+        "c2": ((1, 8192, 8192, 8192, 14, True), (1, 256, 256, 1, 1, 16)),
+        "c2r": ((1, 8192, 8192, 8192, 13, False), (1, 256, 256, 1, 0, 16)),
+        "c3": ((1, 4096, 4096, 4096, 14, True), (1, 256, 256, 1, 1, 32)),
+        "c4": ((64, 512, 512, 512, 14, True), (1, 256, 256, 14, 1, 4)),
+        "c5": ((1, 1023, 2049, 32769, 15, True), (2, 256, 256, 1, 2, 63)),
+        "c5r": ((1, 1023, 2049, 32769, 13, False), (2, 256, 256, 1, 0, 63)),
+    }
+    for name, (shape, want) in forms.items():
+        L = capi.layout(*shape)
+        got = (L.ksplit, L.gemm_tile_rows, L.gemm_tile_cols, L.gemm_run, L.ncorr, L.nslab)
+        assert got == want, (name, got, want)
