@@ -1224,6 +1224,7 @@ struct GemmArgs {
   int P, ncorr, nslots, batch;
   int ksplit;          // groups per output tile, each over a contiguous K range
   int run;             // residue slots per run group (1: one slot per group)
+  int corr_run;        // 1: each tile's run starts with the (fused) correction slot
   int p[kMaxP];
   double invp[kMaxP];
 };
@@ -1315,6 +1316,9 @@ struct GemmShape {
 // correction slots, then the runs of g.run residue slots of each tile (the
 // last run of a tile shorter when g.run does not divide P): a group runs its
 // run's slots back to back (nrun of them) on one stream of operand copies.
+// With g.corr_run (one run of all P residue slots per tile, and the fused
+// correction slot) each tile has one group, whose run starts with the
+// correction slot.
 struct GemmItem {
   int split, slot, nrun, mt, nt;
   int64_t b;
@@ -1332,7 +1336,10 @@ __device__ __forceinline__ GemmItem gemm_item(const GemmArgs& g) {
   const int64_t sb = sbs / g.ksplit;
   const int v = (int)(sb / g.batch);
   it.b = sb - (int64_t)v * g.batch;
-  if (v < g.ncorr) {
+  if (g.corr_run) {
+    it.slot = 0;   // the correction slot, then every residue slot
+    it.nrun = g.nslots;
+  } else if (v < g.ncorr) {
     it.slot = v;
     it.nrun = 1;
   } else {
@@ -1596,12 +1603,43 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     // dependency resolution": reads and writes return in the order issued),
     // so the count reaches kDma only after every operation older than the
     // last kDma -- the stage and everything before it.
-    const int nks = nk, nkr = it.nrun * nk;
-    int cj = 0, ckt = 0;   // the next stage to copy: slot cj of the run, k-step ckt
+    // A run that starts with the correction slot (g.corr_run) streams its
+    // 2 nkt k-steps first, from the correction plane (At, Bt: row-tile stride
+    // 2 nkt; A = [hi | q], B = [q | hi], so the two halves accumulate
+    // without a store between them), then the residue slots from plane 0.
+    const bool crun = is_corr;
+    const int nks = crun ? g.nkt : nk;       // k-steps of a residue slot
+    const int nkc = crun ? 2 * g.nkt : 0;    // k-steps of the correction slot
+    const int8_t* ArA = crun ? g.A + b * g.memberA + (int64_t)mrt * g.nkt * kTileBytes : At;
+    const int8_t* ArB = crun ? g.B + b * g.memberB + (int64_t)nrt * g.nkt * kTileBytes : Bt;
+    const int nkr = nkc + (it.nrun - (crun ? 1 : 0)) * nks;
+    // The next stage to copy: residue slot cj of the run (-1: the correction
+    // slot), k-step ckt.
+    int cj = crun ? -1 : 0, ckt = 0;
     auto next_src = [&]() {
-      cpA = At + (int64_t)cj * g.planeA + (int64_t)ckt * kTileBytes;
-      cpB = Bt + (int64_t)cj * g.planeB + (int64_t)ckt * kTileBytes;
-      if (++ckt == nks) { ckt = 0; ++cj; }
+      if (cj < 0) {
+        cpA = At + (int64_t)ckt * kTileBytes;
+        cpB = Bt + (int64_t)ckt * kTileBytes;
+        if (++ckt == nkc) { ckt = 0; cj = 0; }
+      } else {
+        cpA = ArA + (int64_t)cj * g.planeA + (int64_t)ckt * kTileBytes;
+        cpB = ArB + (int64_t)cj * g.planeB + (int64_t)ckt * kTileBytes;
+        if (++ckt == nks) { ckt = 0; ++cj; }
+      }
+    };
+    auto store_corr = [&]() {
+      int32_t* cdst = g.corr + (b * g.ncorr) * g.outplane;
+#pragma unroll
+      for (int x = 0; x < kWM; ++x)
+#pragma unroll
+        for (int h = 0; h < kHB; ++h) {
+          v4i* d = reinterpret_cast<v4i*>(cdst + ((rb0 + x) * NB + cb0 + h) * 1024 + lane * 16);
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            d[q] = v4i{acc_read(acc[x][4 * h + q][0]), acc_read(acc[x][4 * h + q][1]),
+                       acc_read(acc[x][4 * h + q][2]), acc_read(acc[x][4 * h + q][3])};
+          __builtin_amdgcn_sched_barrier(0);
+        }
     };
     auto store_slot = [&](const int s_) {
       const int t = s_ - g.ncorr;
@@ -1636,26 +1674,29 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
       wait_vm_lgkm0<0>();
       barrier_lds();
       for (int j = 0; j < it.nrun; ++j) {
-        // Slot j: k-steps G0 .. G0 + nks - 1.  Its first stage has landed
+        // Slot j: k-steps G0 .. G0 + nj - 1.  Its first stage has landed
         // and is visible (the wait and barrier of the stream's previous
         // step), and no copy targets it before this slot's first step.
-        const int G0 = j * nks;
+        const bool jc = crun && j == 0;
+        const int nj = jc ? nkc : nks;
+        const int G0 = jc ? 0 : nkc + (j - (crun ? 1 : 0)) * nks;
         v4i F0[kWM + kWN], F1[kWM + kWN];
         FP64EMU_READF(F0, G0);
         FP64EMU_RSTEP(G0, F0, F1, mma16_init);
         int kt = 1;
         const int kf = nk - kPF - G0;   // steps kt < kf copy stage G0 + kt + kPF
-        for (; kt + 2 <= nks && kt + 1 < kf; kt += 2) {
+        for (; kt + 2 <= nj && kt + 1 < kf; kt += 2) {
           FP64EMU_RSTEP_FULL(G0 + kt, F1, F0);
           FP64EMU_RSTEP_FULL(G0 + kt + 1, F0, F1);
         }
-        for (; kt + 2 <= nks; kt += 2) {
+        for (; kt + 2 <= nj; kt += 2) {
           FP64EMU_RSTEP(G0 + kt, F1, F0, mma16);
           FP64EMU_RSTEP(G0 + kt + 1, F0, F1, mma16);
         }
-        if (kt < nks) FP64EMU_RSTEP(G0 + kt, F1, F0, mma16);
+        if (kt < nj) FP64EMU_RSTEP(G0 + kt, F1, F0, mma16);
         mfma_fence();
-        store_slot(slot + j);
+        if (jc) store_corr();
+        else store_slot(slot + j);
       }
 #undef FP64EMU_RSTEP
 #undef FP64EMU_RSTEP_FULL
@@ -2594,9 +2635,12 @@ int run(const Call& c) {
   ga.P = c.P; ga.ncorr = L.ncorr; ga.nslots = c.P + L.ncorr; ga.batch = (int)c.batch;
   ga.ksplit = L.ksplit;
   ga.run = L.gemm_run;
+  // One run of every residue slot per tile, and a fused correction slot: the
+  // run starts with the correction slot (one group per tile).
+  ga.corr_run = (ga.run > 1 && ga.run == c.P && L.ncorr == 1) ? 1 : 0;
   for (int t = 0; t < kMaxP; ++t) { ga.p[t] = tab.p[t]; ga.invp[t] = tab.invp[t]; }
   // Work items per tile: the correction slots, then the residue slots in runs.
-  const int64_t vslots = L.ncorr + (c.P + ga.run - 1) / ga.run;
+  const int64_t vslots = ga.corr_run ? 1 : L.ncorr + (c.P + ga.run - 1) / ga.run;
   ga.total = vslots * c.batch * L.ksplit * ga.TM * ga.TN;
 
   {

@@ -191,7 +191,8 @@ typedef struct {
                                products (at most 32 k-steps, no K-split) on 256 x 256
                                tiles, of which they have T >= 256 (fewer take 256 x 128
                                or 128 x 128 tiles): one run of all nprimes slots when T
-                               is a multiple of 256, three runs otherwise (1 when that
+                               is a multiple of 256 (the fused correction slot then
+                               leads the run), three runs otherwise (1 when that
                                leaves runs of one) */
   int64_t ext_rowsA;        /* rows of each A plane (per member, per row chunk) that the
                                extraction writes: the operand rows and the zero padding
