@@ -1186,7 +1186,8 @@ extract_kernel(ExtractArgs a) {
 // ---------------------------------------------------------------------------
 // Modular GEMM engine.  Work item = (slot, batch member, 256x256 output tile);
 // slot = correction GEMM(s) first (they are twice as deep), then one slot per
-// modulus.  Exact int32 C = A_plane B_plane^T per slot
+// modulus (slot runs group a tile's slots; under one run per tile the fused
+// correction slot leads the run).  Exact int32 C = A_plane B_plane^T per slot
 // (fp64_emu_cuda/fp64_emu.cu:491-657); epilogue: balanced int8 residue for
 // modulus slots (the reference's bal8, :613-620, here as an exact fp64
 // nearest-quotient reduction), raw int32 for correction slots.
