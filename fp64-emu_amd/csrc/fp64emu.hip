@@ -1340,6 +1340,18 @@ __device__ __forceinline__ GemmItem gemm_item(const GemmArgs& g) {
   if (g.corr_run) {
     it.slot = 0;   // the correction slot, then every residue slot
     it.nrun = g.nslots;
+  } else if (g.run > 1) {
+    // Several runs per tile: the runs (the longest groups) first, the
+    // correction slots after them, so that the short groups fill the last
+    // round.
+    const int nr = (g.P + g.run - 1) / g.run;
+    if (v < nr) {
+      it.slot = g.ncorr + v * g.run;
+      it.nrun = min(g.run, g.nslots - it.slot);
+    } else {
+      it.slot = v - nr;
+      it.nrun = 1;
+    }
   } else if (v < g.ncorr) {
     it.slot = v;
     it.nrun = 1;
