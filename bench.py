@@ -72,6 +72,27 @@ def parse():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a float64 streaming kernel over 1 GiB (read 1 GiB, write "
                          "1 GiB) three times: the scale of the FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="only the ceiling probes: the modular GEMM's inner loop with its "
+                         "operands in registers, read from LDS, and fed by its global->LDS "
+                         "copies from L2 (TOP/s and shader clock), and HBM read / write / copy "
+                         "streams (GB/s), as one JSON line")
+    ap.add_argument("--card-grid", action="store_true",
+                    help="only the reference's card protocol (bench/card_bench.py): n = 256 .. "
+                         "16384, native, default plan and reduced plan, median of timed calls, "
+                         "as JSON lines")
+    ap.add_argument("--small-n", action="store_true",
+                    help="only the reference's small-n table (bench/smalln.py): n = 64 .. 512, "
+                         "eager mm against HIP-graph replay of the same call against native, "
+                         "as JSON lines")
+    ap.add_argument("--first-call", action="store_true",
+                    help="only the first-call cost at n = 2048 (the process's first call, the "
+                         "first call of a new shape, steady state), as one JSON line; run it "
+                         "in a fresh process")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="leave roofline.traffic null instead of measuring it with two "
+                         "rocprofv3 --pmc child runs (FETCH_SIZE, WRITE_SIZE) before the timing")
+    ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
     return ap.parse_args()
 
 
@@ -94,6 +115,296 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def _event_ms(fn, torch):
+    """One call of fn bracketed by events on the current stream, in ms."""
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)
+
+
+def measure_ceilings(dev, seconds=0.25):
+    """The rates this part attains, measured by the library's probes
+    (fp64emu_probe_mfma, fp64emu_probe_stream):
+
+    - mfma_registers: the modular GEMM's MFMA loop (one group of 4 waves
+      per CU, 8 x 8 accumulator quads per wave, 64 v_mfma_i32_16x16x64_i8
+      per step in its order) on random balanced residues held in registers:
+      the INT8 rate this part sustains under its power limit;
+    - mfma_lds_reads: the same with the GEMM's fragment reads from its LDS
+      ring and its per-step wait and barrier;
+    - mfma_lds_copies: that plus its global->LDS copies from an L2-resident
+      source: the GEMM's inner loop without HBM traffic, prologue, epilogue
+      or tail.
+    Each is the median of 3 launches of about `seconds`; the shader clock is
+    the median over groups of s_memtime against the 100 MHz s_memrealtime.
+    Then HBM streams over 1 GiB buffers (median of 5): read, write, and
+    read-plus-write (the byte phases' shape)."""
+    import statistics
+    import numpy as np
+    import torch
+    from fp64_emu import capi
+    groups = torch.cuda.get_device_properties(dev).multi_processor_count
+    src = torch.from_numpy(capi.probe_source(11)).to(dev)
+    ops_per_step = groups * 4 * 64 * 16 * 16 * 64 * 2
+    out = {"groups": groups}
+    for mode, name in ((0, "mfma_registers"), (1, "mfma_lds_reads"), (2, "mfma_lds_copies")):
+        steps = 2001
+        capi.probe_mfma(src, groups, steps, mode)          # warm-up
+        t = _event_ms(lambda: capi.probe_mfma(src, groups, steps, mode), torch)
+        steps = max(2001, int(steps * seconds * 1e3 / t)) | 1
+        ts, ghz = [], []
+        for _ in range(3):
+            res = {}
+
+            def run():
+                res["clk"] = capi.probe_mfma(src, groups, steps, mode)[1]
+            ts.append(_event_ms(run, torch))
+            c = res["clk"].cpu().numpy().astype(np.float64)
+            ghz.append(float(np.median((c[:, 1] - c[:, 0]) / (c[:, 3] - c[:, 2]) * 0.1)))
+        t = statistics.median(ts)
+        out[name] = {"tops": round(ops_per_step * steps / (t * 1e-3) / 1e12, 1),
+                     "clock_ghz": round(statistics.median(ghz), 3), "steps": steps,
+                     "ms": round(t, 3)}
+    n = (1 << 30) // 8
+    a = torch.ones(n, dtype=torch.float64, device=dev)
+    b = torch.empty_like(a)
+    for mode, name, nbytes in ((0, "hbm_read", 8 * n), (1, "hbm_write", 8 * n),
+                               (2, "hbm_copy", 16 * n)):
+        for _ in range(2):
+            capi.probe_stream(b, a, mode)
+        t = statistics.median(_event_ms(lambda: capi.probe_stream(b, a, mode), torch)
+                              for _ in range(5))
+        out[name] = {"gbs": round(nbytes / (t * 1e-3) / 1e9, 1), "ms": round(t, 4),
+                     "bytes": nbytes}
+    del a, b
+    torch.cuda.empty_cache()
+    return out
+
+
+def traffic_child(n):
+    """Run under rocprofv3 --pmc by measure_traffic: the copy probe over
+    1 GiB (known bytes, the counters' scale), then two c2 calls."""
+    import torch
+    import fp64_emu
+    from fp64_emu import capi
+    dev = torch.device("cuda:0")
+    m = (1 << 30) // 8
+    a = torch.ones(m, dtype=torch.float64, device=dev)
+    b = torch.empty_like(a)
+    capi.probe_stream(b, a, 2)
+    torch.cuda.synchronize()
+    del a, b
+    g = torch.Generator().manual_seed(2000)
+    A = torch.randn(n, n, dtype=torch.float64, generator=g).to(dev)
+    g = torch.Generator().manual_seed(2001)
+    Bt = torch.randn(n, n, dtype=torch.float64, generator=g).to(dev)
+    for _ in range(2):
+        fp64_emu.mm_nt(A, Bt)
+    torch.cuda.synchronize()
+    print("traffic child done", flush=True)
+
+
+def measure_traffic(n, timeout=240):
+    """The modular GEMM's traffic across the L2 boundary per launch (reads
+    from MALL or HBM plus writes), from two rocprofv3 --pmc child runs of
+    traffic_child: FETCH_SIZE, then WRITE_SIZE (KiB per dispatch), each
+    scaled by what the same counter reads for the copy probe's 1 GiB read
+    and 1 GiB write in that run.  None (with the reason logged) when
+    rocprofv3 is missing or a run fails."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        log("traffic: rocprofv3 not found")
+        return None
+    res = {}
+    env = dict(os.environ, TMPDIR="/tmp")
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="fp64emu_pmc_", dir="/tmp")
+        cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "t", "--",
+               sys.executable, os.path.abspath(__file__), "--traffic-child", "--n", str(n)]
+        log(f"traffic: {counter} child run")
+        try:
+            r = subprocess.run(cmd, cwd="/tmp", env=env, timeout=timeout, capture_output=True,
+                               text=True)
+        except subprocess.TimeoutExpired:
+            log(f"traffic: {counter} run timed out")
+            return None
+        files = [os.path.join(dp, f) for dp, _, fs in os.walk(d) for f in fs
+                 if f.endswith("counter_collection.csv")]
+        if r.returncode != 0 or "traffic child done" not in r.stdout or not files:
+            log(f"traffic: {counter} run failed (rc {r.returncode}): {r.stderr[-300:]}")
+            return None
+        gemm, copy = [], []
+        with open(files[0]) as f:
+            for row in csv.DictReader(f):
+                if row["Counter_Name"] != counter:
+                    continue
+                if "modgemm_kernel" in row["Kernel_Name"]:
+                    gemm.append(float(row["Counter_Value"]))
+                elif "stream_probe_kernel<2>" in row["Kernel_Name"]:
+                    copy.append(float(row["Counter_Value"]))
+        shutil.rmtree(d, ignore_errors=True)
+        if not gemm or len(copy) != 1:
+            log(f"traffic: {counter}: no dispatches found")
+            return None
+        scale = copy[0] * 1024 / float(1 << 30)     # counter KiB per true byte / 1024
+        res[counter] = {"kib_per_dispatch": round(sum(gemm) / len(gemm), 1),
+                        "dispatches": len(gemm), "copy_probe_kib": round(copy[0], 1),
+                        "scale": round(scale, 5),
+                        "bytes": int(sum(gemm) / len(gemm) * 1024 / scale)}
+    total = res["FETCH_SIZE"]["bytes"] + res["WRITE_SIZE"]["bytes"]
+    log(f"traffic: {res['FETCH_SIZE']['bytes'] / 1e9:.2f} GB fetched + "
+        f"{res['WRITE_SIZE']['bytes'] / 1e9:.2f} GB written per GEMM launch")
+    return {"bytes_per_launch": total, "counters": res,
+            "method": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE child runs of this script "
+                      "(--traffic-child: the copy probe over 1 GiB for the scale, then two c2 "
+                      "calls), averaged over the modgemm dispatches"}
+
+
+def card_grid():
+    """The reference's card protocol (bench/card_bench.py:14-44, README.md:
+    125-138): n = 256 .. 16384, randn operands (CPU seeds 8000 + n), native
+    float64 matmul (rocBLAS) and the emulated mm at the default plan
+    (plan_config(n)) and the reduced plan (one modulus fewer, no
+    correction), each the median of timed calls (host clock, a
+    synchronisation per call, after 3 warm-ups; 30 calls up to n = 1024, 3
+    at 16384, else 8; native half as many, at least 3)."""
+    import statistics
+    import torch
+    import fp64_emu
+    dev = torch.device("cuda:0")
+    pin_rocblas()
+
+    def timed(fn, iters, warmup=3):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(iters):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    for n in (256, 1024, 2048, 4096, 8192, 16384):
+        flop = 2.0 * n ** 3
+        it = 3 if n >= 16384 else (30 if n <= 1024 else 8)
+        g = torch.Generator().manual_seed(8000 + n)
+        A = torch.randn(n, n, dtype=torch.float64, generator=g).to(dev)
+        Bt = torch.randn(n, n, dtype=torch.float64, generator=g).to(dev)
+        B = Bt.t().contiguous()
+        tn = timed(lambda: A @ Bt, max(3, it // 2))
+        P, corr = fp64_emu.plan_config(n)
+        rec = {"table": "card_grid", "n": n, "native": {"ms": round(tn * 1e3, 4),
+                                                       "tflops": round(flop / tn / 1e12, 2)}}
+        for cfg, pp, cc in (("default", P, corr), ("reduced", P - 1, False)):
+            t = timed(lambda: fp64_emu.mm(A, B, nprimes=pp, corr=cc), it)
+            rec[cfg] = {"plan": [pp, cc], "ms": round(t * 1e3, 4),
+                        "tflops": round(flop / t / 1e12, 2), "x_native": round(tn / t, 2)}
+        print(json.dumps(rec), flush=True)
+        del A, Bt, B
+        torch.cuda.empty_cache()
+
+
+def small_n():
+    """The reference's small-n table (bench/smalln.py:29-50, paper.tex:
+    650-652): n = 64 .. 512, randn A and B (CPU seeds), the emulated mm
+    eager against a HIP-graph replay of the same call against native
+    float64 matmul, each the median of 200 host-timed calls (a
+    synchronisation per call) after 20 warm-ups; the replay's output is
+    checked against an eager call."""
+    import statistics
+    import torch
+    import fp64_emu
+    dev = torch.device("cuda:0")
+    pin_rocblas()
+
+    def timed(fn, iters=200, warm=20):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(iters):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    for n in (64, 128, 256, 512):
+        g = torch.Generator().manual_seed(8500 + n)
+        A = torch.randn(n, n, dtype=torch.float64, generator=g).to(dev)
+        B = torch.randn(n, n, dtype=torch.float64, generator=g).to(dev)
+        te = timed(lambda: fp64_emu.mm(A, B))
+        tn = timed(lambda: A @ B.t())
+        for _ in range(3):
+            fp64_emu.mm(A, B)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            C = fp64_emu.mm(A, B)
+        graph.replay()
+        torch.cuda.synchronize()
+        ok = bool(torch.equal(C, fp64_emu.mm(A, B)))
+        tg = timed(graph.replay)
+        print(json.dumps({"table": "small_n", "n": n, "eager_us": round(te * 1e6, 1),
+                          "graph_us": round(tg * 1e6, 1), "native_us": round(tn * 1e6, 1),
+                          "eager_over_graph": round(te / tg, 2),
+                          "graph_vs_native": round(tn / tg, 2), "graph_equals_eager": ok}),
+              flush=True)
+        del graph, C, A, B
+        torch.cuda.empty_cache()
+
+
+def first_call():
+    """First-call cost (paper.tex:674-677 reports the reference's first call
+    at a new shape, which runs its dispatch probe: 16.6 ms against 1.41 ms
+    steady at n = 2048).  This build keeps no per-shape state, so a first
+    call costs the workspace allocation plus, once per process, the loading
+    of the library's code objects.  In this process, with resident randn
+    operands: (1) the process's first emulated mm call (n = 1024), (2) the
+    1024 steady state, (3) after torch's cached blocks are released, the
+    first call at the new shape n = 2048, (4) the 2048 steady state, the
+    median of 20 calls; host clock, a synchronisation per call.  Run it as
+    its own process."""
+    import statistics
+    import torch
+    import fp64_emu
+    dev = torch.device("cuda:0")
+
+    def once(fn):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3
+
+    g = torch.Generator().manual_seed(8900)
+    A = torch.randn(2048, 2048, dtype=torch.float64, generator=g).to(dev)
+    B = torch.randn(2048, 2048, dtype=torch.float64, generator=g).to(dev)
+    a, b = A[:1024, :1024].contiguous(), B[:1024, :1024].contiguous()
+    torch.cuda.synchronize()
+    first = once(lambda: fp64_emu.mm(a, b))
+    steady_1024 = statistics.median(once(lambda: fp64_emu.mm(a, b)) for _ in range(20))
+    torch.cuda.empty_cache()
+    new_shape = once(lambda: fp64_emu.mm(A, B))
+    steady = statistics.median(once(lambda: fp64_emu.mm(A, B)) for _ in range(20))
+    print(json.dumps({"table": "first_call", "process_first_ms_n1024": round(first, 3),
+                      "steady_ms_n1024": round(steady_1024, 3),
+                      "new_shape_first_ms_n2048": round(new_shape, 3),
+                      "steady_ms_n2048": round(steady, 3),
+                      "process_first_over_steady": round(first / steady_1024, 2),
+                      "new_shape_over_steady": round(new_shape / steady, 2)}), flush=True)
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -102,8 +413,25 @@ def main():
               "multi-GPU path); use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
+    if args.traffic_child:
+        traffic_child(args.n)
+        return
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.ceilings:
+        import torch
+        print(json.dumps({"table": "ceilings", **measure_ceilings(torch.device("cuda:0"))}),
+              flush=True)
+        return
+    if args.card_grid:
+        card_grid()
+        return
+    if args.small_n:
+        small_n()
+        return
+    if args.first_call:
+        first_call()
         return
     if args.accuracy_grid:
         accuracy_grid()
@@ -118,6 +446,12 @@ def main():
         run_configs(max(args.steps, 3), max(args.warmup, 1),
                     [args.config] if args.config else CONFIG_NAMES)
         return
+
+    # The modular GEMM's L2-boundary traffic per launch, counted in two
+    # rocprofv3 child runs before this process touches the GPU.
+    traffic = None
+    if not args.no_traffic:
+        traffic = measure_traffic(args.n)
 
     import torch
     import fp64_emu
@@ -161,7 +495,15 @@ def main():
     avg = [sum(p[i] for p in phases) / len(phases) for i in range(4)]
     gemm_ms = avg[1]    # events 1 -> 2 bracket exactly the one modgemm launch
     gemm_tops = 2.0 * M * N * K * G / (gemm_ms * 1e-3) / 1e12
-    log(f"phases ms (avg of {len(phases)}): {['%.3f' % x for x in avg]}")
+    # Per call, events 0 -> 4 bracket the whole call on the device: the
+    # median call (BASELINE's protocol) beside the mean of the wall clock.
+    calls = sorted(sum(p) for p in phases)
+    med_ms = calls[len(calls) // 2] if len(calls) % 2 else 0.5 * (
+        calls[len(calls) // 2 - 1] + calls[len(calls) // 2])
+    gemms = sorted(p[1] for p in phases)
+    med_gemm_ms = gemms[len(gemms) // 2]
+    log(f"phases ms (avg of {len(phases)}): {['%.3f' % x for x in avg]}; median call "
+        f"{med_ms:.3f} ms")
     del ws, evs
 
     # The same step through the drop-in torch op (workspace from torch's
@@ -207,6 +549,15 @@ def main():
         log(f"correct bits: emu {acc['correct_bits_emu']}, native {acc['correct_bits_native']}")
     del Cn
 
+    # The attainable rates of this part, measured in the same run after the
+    # timed calls (the probes run the chip at its power limit).
+    ceil = measure_ceilings(dev)
+    mfma_ceiling = ceil["mfma_registers"]["tops"]
+    log(f"ceilings: MFMA in registers {mfma_ceiling:.0f} TOP/s at "
+        f"{ceil['mfma_registers']['clock_ghz']:.2f} GHz, with LDS reads "
+        f"{ceil['mfma_lds_reads']['tops']:.0f}, with copies {ceil['mfma_lds_copies']['tops']:.0f}; "
+        f"HBM copy {ceil['hbm_copy']['gbs']:.0f} GB/s")
+
     cpu = None
     cpu_torch = None
     if not args.no_cpu:
@@ -225,12 +576,6 @@ def main():
             log(f"config {r['config']}: {r['ms']:.3f} ms, {r['tflops']:.2f} TFLOP/s, "
                 f"{r['tflops'] / r['native_tflops']:.2f}x native, bits {r['correct_bits_emu']} / "
                 f"{r['correct_bits_native']}")
-
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "modgemm_c2_traffic.json")
-    if n == 8192 and os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
 
     rec = {
         "metric": METRIC,
@@ -252,9 +597,16 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "modgemm_kernel",
                      "achieved": round(gemm_tops, 1), "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
-                     "traffic": traffic,
-                     "work": "2*M*N*K*G INT8 ops per launch"},
+                     "traffic": traffic["bytes_per_launch"] if traffic else None,
+                     "work": "2*M*N*K*G INT8 ops per launch",
+                     "measured_peak": round(mfma_ceiling, 1),
+                     "frac_of_measured": round(gemm_tops / mfma_ceiling, 4),
+                     "measured_loop": round(ceil["mfma_lds_copies"]["tops"], 1),
+                     "frac_of_measured_loop": round(gemm_tops / ceil["mfma_lds_copies"]["tops"], 4)},
         "plan_roofline_frac": round(value / (INT8_PEAK_TOPS / G), 4),
+        "median_call_ms": round(med_ms, 4),
+        "value_at_median_call": round(flop / (med_ms * 1e-3) / 1e12, 3),
+        "median_gemm_ms": round(med_gemm_ms, 4),
         "phases_ms": [round(x, 4) for x in avg],
         "torch_op_ms_per_step": round(op_ms, 4),
         "native_dgemm_tflops": round(nat_tf, 2),
@@ -263,6 +615,8 @@ def main():
         **acc,
         "cpu_baseline": cpu,
         "cpu_torch_f64": cpu_torch,
+        "ceilings": ceil,
+        "traffic": traffic,
         "native_blas": native_blas(),
         "configs": configs,
     }
@@ -474,19 +828,22 @@ def run_configs(steps, warmup, names, emit=True):
 
         ms = timed(emu)
         nat_ms = timed(nat)
-        phases = None
-        if not batched:
-            primes = fp64_emu._PRIMES[:P]
-            lay = capi.layout(1, M, N, K, P, corr)
-            ws = torch.empty(int(lay.total), dtype=torch.uint8, device=dev)
-            C = torch.empty(M, N, dtype=torch.float64, device=dev)
-            evs = [capi.PhaseEvents() for _ in range(steps)]
-            for i in range(steps):
+        # Per-phase times: events at the phase boundaries of each call
+        # (fp64emu_mm_nt_events / fp64emu_bmm_nt_events), averaged.
+        primes = fp64_emu._PRIMES[:P]
+        lay = capi.layout(batch, M, N, K, P, corr)
+        ws = torch.empty(int(lay.total), dtype=torch.uint8, device=dev)
+        C = torch.empty((batch, M, N) if batched else (M, N), dtype=torch.float64, device=dev)
+        evs = [capi.PhaseEvents() for _ in range(steps)]
+        for i in range(steps):
+            if batched:
+                capi.bmm_nt_events(A, B, primes, C, ws, evs[i], use_corr=corr, exact=exact)
+            else:
                 capi.mm_nt_events(A, B, primes, C, ws, evs[i], use_corr=corr, exact=exact)
-            torch.cuda.synchronize()
-            ph = [e.phases_ms() for e in evs]
-            phases = [round(sum(p[i] for p in ph) / len(ph), 4) for i in range(4)]
-            del ws, C, evs
+        torch.cuda.synchronize()
+        ph = [e.phases_ms() for e in evs]
+        phases = [round(sum(p[i] for p in ph) / len(ph), 4) for i in range(4)]
+        del ws, C, evs
         Ce, Cn = emu(), nat()
         bits = {}
         for tag, X in (("emu", Ce), ("native", Cn)):

@@ -1305,6 +1305,12 @@ struct GemmShape {
   static constexpr int kDma = kWM / 2 + kWN / 2;                  // copies per wave per stage
   static constexpr int kHB = kWN / 4;                             // 64-column output blocks per wave
   static constexpr int kGroupsPerCU = (kWM == 8 && kWN == 8) ? 1 : 2;
+  // The ring is the kernels' static LDS array: it must fit one CU's 160 KiB
+  // for every group the shape puts there.  (No kernel of this library takes
+  // dynamic LDS: a launch would need hipFuncAttributeMaxDynamicSharedMemorySize
+  // set and checked above 64 KiB.)
+  static constexpr int kLdsBytes = kS * kSB;
+  static_assert(kLdsBytes * kGroupsPerCU <= 160 * 1024, "LDS ring exceeds the CU's 160 KiB");
 };
 
 // Work item of a group: XCD-aware order -- work group i runs on XCD i % 8;
@@ -1871,7 +1877,7 @@ __global__ void __launch_bounds__(kThreads, (kWM == 8 && kWN == 8) ? 1 : 2)
 modgemm_kernel(GemmArgs g) {
   static_assert(!kRun || (kWM == 8 && kWN == 8), "slot runs: 256 x 256 tiles only");
   using Sh = GemmShape<kWM, kWN>;
-  __shared__ __attribute__((aligned(1024))) int8_t lds[Sh::kS * Sh::kSB];
+  __shared__ __attribute__((aligned(1024))) int8_t lds[Sh::kLdsBytes];
   const GemmItem it = gemm_item(g);
   if constexpr (kRun) {
     if (it.nrun > 1) {
@@ -1887,7 +1893,7 @@ modgemm_kernel(GemmArgs g) {
 // (half the MFMA work of a 256-column tile of mostly padding).
 __global__ void __launch_bounds__(kThreads, 1)
 modgemm_mixed_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) int8_t lds[GemmShape<8, 8>::kS * GemmShape<8, 8>::kSB];
+  __shared__ __attribute__((aligned(1024))) int8_t lds[GemmShape<8, 8>::kLdsBytes];
   GemmItem it = gemm_item(g);
   if (it.nt == g.TN - 1) {
     it.nt *= 2;
@@ -2481,6 +2487,181 @@ ddgemm_nt_kernel(double* __restrict__ hi, double* __restrict__ lo, const double*
 }
 
 // ---------------------------------------------------------------------------
+// Ceiling probes (not on the product path): the rates this part attains, for
+// the benchmark to set the modular GEMM and the byte phases against.
+//
+// mfma_probe_kernel<kMode>: the modular GEMM's work-group shape and inner
+// loop without its data: 4 waves (one per SIMD, one group per CU), each
+// with 8 x 8 accumulator quads, 64 v_mfma_i32_16x16x64_i8 per step in the
+// GEMM's serpentine order, on fragments that alternate between two stages
+// of the source (A tile, then B tile, 32 KiB each, in the planes' fragment
+// order).
+//   kMode 0: both stages' fragments stay in registers (no memory traffic).
+//   kMode 1: the next step's 16 fragments are read from the GEMM's 4-stage
+//            LDS ring as the GEMM reads them (one per 4 MFMAs), with the
+//            per-step wait and barrier.
+//   kMode 2: kMode 1 plus the GEMM's direct global->LDS copies of the stage
+//            three steps ahead (8 of 1 KiB per wave per step) from the 64 KiB
+//            source, which every L2 holds: the GEMM's inner loop without
+//            HBM or fabric traffic, prologue, epilogue or tail.
+// Ring slot q holds stage q mod 2 throughout (the copies rewrite the same
+// bytes), so after `steps` steps every accumulator holds the sum of the
+// stages' products: the benchmark's source makes stage 1's A tile the
+// negation of stage 0's, so an even step count leaves zeros and an odd one
+// stage 0's product, which the tests check element by element.  Group 0
+// stores its accumulators ([wave][x][y] blocks of 256 int32, lane l's value
+// v at 4 l + v).  Thread 0 of each group records s_memtime (shader clock)
+// and s_memrealtime (100 MHz) after the first barrier and after the loop.
+template <int kMode>
+__global__ void __launch_bounds__(kThreads, 1)
+mfma_probe_kernel(const int8_t* __restrict__ src, int64_t steps, int32_t* __restrict__ acc_out,
+                  unsigned long long* __restrict__ clk) {
+  constexpr int kS = 4, kSB = 2 * kTileBytes;
+  __shared__ __attribute__((aligned(1024))) int8_t lds[kMode == 0 ? 16 : kS * kSB];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  v4i F0[16], F1[16];
+  v4i acc[8][8];
+  // Fragment f of stage s: f < 8 is A row block 8 wm + f, else B column
+  // block 8 wn + f - 8.
+  auto src_frag = [&](int s, int f) -> v4i {
+    const v4i* p = reinterpret_cast<const v4i*>(src + s * kSB);
+    return f < 8 ? p[(wm * 8 + f) * 64 + lane] : p[kTileBytes / 16 + (wn * 8 + f - 8) * 64 + lane];
+  };
+  if constexpr (kMode == 0) {
+#pragma unroll
+    for (int f = 0; f < 16; ++f) {
+      F0[f] = src_frag(0, f);
+      F1[f] = src_frag(1, f);
+    }
+  } else {
+    // Every ring slot q gets stage q mod 2: 4 x 32 KiB, 512 bytes per thread.
+    const v4i* s4 = reinterpret_cast<const v4i*>(src);
+    v4i* l4 = reinterpret_cast<v4i*>(lds);
+#pragma unroll 4
+    for (int i = tid; i < kS * kSB / 16; i += kThreads) l4[i] = s4[i % (2 * kSB / 16)];
+    __syncthreads();
+    const v4i* sl = reinterpret_cast<const v4i*>(lds);
+#pragma unroll
+    for (int f = 0; f < 16; ++f)
+      F0[f] = f < 8 ? sl[(wm * 8 + f) * 64 + lane] : sl[kTileBytes / 16 + (wn * 8 + f - 8) * 64 + lane];
+  }
+  __syncthreads();
+  unsigned long long t0 = 0, r0 = 0;
+  if (tid == 0) {
+    t0 = __builtin_amdgcn_s_memtime();
+    r0 = __builtin_amdgcn_s_memrealtime();
+  }
+  const uint32_t goff = (uint32_t)(wave * 4096 + lane * 16);
+  // One step: the MFMAs on FC, in modes 1 and 2 the next step's fragments
+  // into FN from ring slot (kt + 1) mod 4 and (mode 2) the copies of stage
+  // kt + 3 into slot (kt + 3) mod 4, spread as in the GEMM.
+  auto step = [&](const int64_t kt, v4i(&FC)[16], v4i(&FN)[16], auto first) {
+    if constexpr (kMode != 0) {
+      wait_vm_lgkm0<kMode == 2 ? 8 : 0>();
+      barrier_lds();
+    }
+    const v4i* sa = reinterpret_cast<const v4i*>(lds + ((kt + 1) & 3) * kSB);
+    const v4i* sb = sa + kTileBytes / 16;
+    const int8_t* cg = src + ((kt + 3) & 1) * kSB + goff;
+    lds_i8* cl = (lds_i8*)(lds + ((kt + 3) & 3) * kSB + wave * 4096);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (kMode == 2) {
+          const int half = (c >> 1) * kTileBytes;   // chunks 0, 1 copy A; 2, 3 copy B
+          // (The builtin's offset must be a literal.)
+          if (j == 0 && !(c & 1)) __builtin_amdgcn_global_load_lds(cg + half, cl + half, 16, 0, 0);
+          if (j == 2 && !(c & 1)) __builtin_amdgcn_global_load_lds(cg + half, cl + half, 16, 1024, 0);
+          if (j == 0 && (c & 1)) __builtin_amdgcn_global_load_lds(cg + half, cl + half, 16, 2048, 0);
+          if (j == 2 && (c & 1)) __builtin_amdgcn_global_load_lds(cg + half, cl + half, 16, 3072, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (kMode != 0) {
+          const int f = c * 4 + j;
+          if (f < 8) FN[8 + f] = sb[(wn * 8 + f) * 64 + lane];
+          else FN[f - 8] = sa[(wm * 8 + f - 8) * 64 + lane];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int m = 4 * j + u, x = c * 2 + m / 8, y = (m < 8) ? m : 15 - m;
+          if constexpr (decltype(first)::value) mma16_init(acc[x][y], FC[x], FC[8 + y]);
+          else mma16(acc[x][y], FC[x], FC[8 + y]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+  };
+  // Modes 1, 2 read step kt + 1's fragments during step kt; mode 0's second
+  // set is stage 1 from the start.
+  step(0, F0, F1, std::true_type{});
+  int64_t kt = 1;
+  for (; kt + 2 <= steps; kt += 2) {
+    step(kt, F1, F0, std::false_type{});
+    step(kt + 1, F0, F1, std::false_type{});
+  }
+  if (kt < steps) step(kt, F1, F0, std::false_type{});
+  wait_vm_lgkm0<0>();
+  mfma_fence();
+  if (tid == 0) {
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+    unsigned long long* c = clk + (int64_t)blockIdx.x * 4;
+    c[0] = t0; c[1] = t1; c[2] = r0; c[3] = r1;
+  }
+  if (blockIdx.x == 0) {
+#pragma unroll
+    for (int x = 0; x < 8; ++x)
+#pragma unroll
+      for (int y = 0; y < 8; ++y) {
+        int32_t* d = acc_out + ((wave * 8 + x) * 8 + y) * 256 + lane * 4;
+        *reinterpret_cast<v4i*>(d) = v4i{acc_read(acc[x][y][0]), acc_read(acc[x][y][1]),
+                                         acc_read(acc[x][y][2]), acc_read(acc[x][y][3])};
+      }
+  }
+}
+
+// stream_probe_kernel<kMode>: HBM streaming over n doubles, 16 bytes per lane
+// per access and four accesses in flight per lane, grid-stride.  kMode 0
+// reads (each group's sum to dst[group]), 1 writes dst = v, 2 copies
+// dst = -src (read plus write, the shape of the extraction and the
+// reconstruction).
+template <int kMode>
+__global__ void __launch_bounds__(kThreads)
+stream_probe_kernel(double* __restrict__ dst, const double* __restrict__ src, int64_t n2, double v) {
+  typedef double v2d __attribute__((ext_vector_type(2)));
+  const v2d* s = reinterpret_cast<const v2d*>(src);
+  v2d* d = reinterpret_cast<v2d*>(dst);
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  v2d sum = v2d{0.0, 0.0};
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n2; i += 4 * stride) {
+    v2d x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (kMode != 1 && i + u * stride < n2) x[u] = s[i + u * stride];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (i + u * stride >= n2) continue;
+      if constexpr (kMode == 0) sum += x[u];
+      else if constexpr (kMode == 1) d[i + u * stride] = v2d{v, v};
+      else d[i + u * stride] = -x[u];
+    }
+  }
+  if constexpr (kMode == 0) {
+    __shared__ double red[kThreads];
+    red[threadIdx.x] = sum.x + sum.y;
+    __syncthreads();
+    for (int w = kThreads / 2; w > 0; w >>= 1) {
+      if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) dst[blockIdx.x] = red[0];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host orchestration.  fp64_emu_cuda/fp64_emu.cu:1127-1186, 1220-1270,
 // 1343-1407 (the fused slice): sizing -> extraction -> modular GEMMs ->
 // reconstruction on one stream, phase events when requested.
@@ -2998,6 +3179,25 @@ int fp64emu_mm_nt_events(double* out, const double* A, const double* Bt, int64_t
   return run(c);
 }
 
+int fp64emu_bmm_nt_events(double* out, const double* A, const double* Bt, int64_t batch, int64_t M,
+                          int64_t N, int64_t K, const int32_t* primes, const int32_t* inv,
+                          const int64_t* mu, int nprimes, int exact, int64_t bits, int use_corr,
+                          void* workspace, size_t workspace_bytes, fp64emu_stream_t stream,
+                          const fp64emu_event_t* events) {
+  (void)inv; (void)mu;
+  g_err.clear();
+  if (!events) return fail(FP64EMU_EINVAL, "events must not be NULL");
+  hipEvent_t ev[5];
+  for (int i = 0; i < 5; ++i) {
+    if (!events[i]) return fail(FP64EMU_EINVAL, "events must not be NULL");
+    ev[i] = reinterpret_cast<hipEvent_t>(events[i]);
+  }
+  Call c = make_call(out, A, Bt, batch, M, N, K, true, primes, nprimes, exact, bits, use_corr,
+                     workspace, workspace_bytes, stream);
+  c.ev = ev;
+  return run(c);
+}
+
 int fp64emu_mm_nt_noalloc(double* out, const double* A, const double* Bt, int64_t M, int64_t N,
                           int64_t K, const int32_t* primes, const int32_t* inv,
                           const int64_t* mu, int nprimes, int exact, int64_t bits,
@@ -3034,6 +3234,43 @@ int fp64emu_ddgemm_nt(double* hi, double* lo, const double* A, const double* B, 
   hipLaunchKernelGGL(ddgemm_nt_kernel, grid, dim3(kThreads), 0,
                      reinterpret_cast<hipStream_t>(stream), hi, lo, A, B, M, N, K);
   return check_hip(hipGetLastError(), "ddgemm launch");
+}
+
+int fp64emu_probe_mfma(int32_t* acc_out, unsigned long long* clocks, const int8_t* src,
+                       int64_t groups, int64_t steps, int mode, fp64emu_stream_t stream) {
+  g_err.clear();
+  if (!acc_out || !clocks || !src) return fail(FP64EMU_EINVAL, "null probe pointer");
+  if (groups < 1 || groups > 65536) return fail(FP64EMU_EINVAL, "probe groups must be in [1, 65536]");
+  if (steps < 1) return fail(FP64EMU_EINVAL, "probe steps must be >= 1");
+  if (reinterpret_cast<uintptr_t>(src) % 16 || reinterpret_cast<uintptr_t>(acc_out) % 16)
+    return fail(FP64EMU_EINVAL, "probe buffers must be 16-byte aligned");
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)groups);
+  switch (mode) {
+    case 0: hipLaunchKernelGGL(mfma_probe_kernel<0>, grid, dim3(kThreads), 0, s, src, steps, acc_out, clocks); break;
+    case 1: hipLaunchKernelGGL(mfma_probe_kernel<1>, grid, dim3(kThreads), 0, s, src, steps, acc_out, clocks); break;
+    case 2: hipLaunchKernelGGL(mfma_probe_kernel<2>, grid, dim3(kThreads), 0, s, src, steps, acc_out, clocks); break;
+    default: return fail(FP64EMU_EINVAL, "probe mode must be 0, 1 or 2");
+  }
+  return check_hip(hipGetLastError(), "probe launch");
+}
+
+int fp64emu_probe_stream(double* dst, const double* src, int64_t n, int mode,
+                         fp64emu_stream_t stream) {
+  g_err.clear();
+  if (mode < 0 || mode > 2) return fail(FP64EMU_EINVAL, "probe mode must be 0, 1 or 2");
+  if (n < 2048 || n % 2) return fail(FP64EMU_EINVAL, "probe length must be even and >= 2048");
+  if (!dst || (mode != 1 && !src)) return fail(FP64EMU_EINVAL, "null probe pointer");
+  if (reinterpret_cast<uintptr_t>(dst) % 16 || reinterpret_cast<uintptr_t>(src) % 16)
+    return fail(FP64EMU_EINVAL, "probe buffers must be 16-byte aligned");
+  const int64_t n2 = n / 2;
+  // n >= 2048 groups' worth: a read's per-group sums fit in dst.
+  const dim3 grid((unsigned)std::min<int64_t>(std::max<int64_t>(n2 / 1024, 1), 4096));
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (mode == 0) hipLaunchKernelGGL(stream_probe_kernel<0>, grid, dim3(kThreads), 0, s, dst, src, n2, 0.0);
+  else if (mode == 1) hipLaunchKernelGGL(stream_probe_kernel<1>, grid, dim3(kThreads), 0, s, dst, src, n2, 1.0);
+  else hipLaunchKernelGGL(stream_probe_kernel<2>, grid, dim3(kThreads), 0, s, dst, src, n2, 0.0);
+  return check_hip(hipGetLastError(), "probe launch");
 }
 
 }  // extern "C"

@@ -23,8 +23,9 @@ TILE_R, TILE_K, FRAG = 256, 64, 1024
 EXPORTS = ("fp64emu_maxp", "fp64emu_last_error", "fp64emu_workspace_size",
            "fp64emu_workspace_size_min", "fp64emu_mm",
            "fp64emu_mm_nt", "fp64emu_bmm", "fp64emu_bmm_nt", "fp64emu_mm_timed",
-           "fp64emu_mm_nt_events", "fp64emu_mm_nt_noalloc", "fp64emu_layout",
-           "fp64emu_ddgemm_nt")
+           "fp64emu_mm_nt_events", "fp64emu_bmm_nt_events", "fp64emu_mm_nt_noalloc",
+           "fp64emu_layout",
+           "fp64emu_ddgemm_nt", "fp64emu_probe_mfma", "fp64emu_probe_stream")
 
 NOALLOC_SCRATCH_BYTES = 64 << 20   # FP64EMU_NOALLOC_SCRATCH_BYTES
 
@@ -77,6 +78,8 @@ def lib():
     L.fp64emu_mm_timed.restype = i32
     L.fp64emu_mm_nt_events.argtypes = mm_args + [ctypes.POINTER(ctypes.c_void_p)]
     L.fp64emu_mm_nt_events.restype = i32
+    L.fp64emu_bmm_nt_events.argtypes = bmm_args + [ctypes.POINTER(ctypes.c_void_p)]
+    L.fp64emu_bmm_nt_events.restype = i32
     L.fp64emu_mm_nt_noalloc.argtypes = [vp, vp, vp, i64, i64, i64, vp, vp, vp, i32, i32, i64,
                                         i32, vp]
     L.fp64emu_mm_nt_noalloc.restype = i32
@@ -84,6 +87,10 @@ def lib():
     L.fp64emu_layout.restype = i32
     L.fp64emu_ddgemm_nt.argtypes = [vp, vp, vp, vp, i64, i64, i64, vp]
     L.fp64emu_ddgemm_nt.restype = i32
+    L.fp64emu_probe_mfma.argtypes = [vp, vp, vp, i64, i64, i32, vp]
+    L.fp64emu_probe_mfma.restype = i32
+    L.fp64emu_probe_stream.argtypes = [vp, vp, i64, i32, vp]
+    L.fp64emu_probe_stream.restype = i32
     _LIB = L
     return L
 
@@ -228,11 +235,32 @@ class PhaseEvents:
                     _HIP.hipEventDestroy(h)
 
 
+def _check_nt(name, A, Bt, out=None, b_nk=False):
+    """The extents a C entry point reads through bare pointers, checked
+    against the tensors before the call: 2-D contiguous float64 operands on
+    one GPU, A [M, K] against Bt [K, N] (or B [N, K] with b_nk), and `out`
+    contiguous float64 [M, N] on that GPU.  Returns (M, N, K)."""
+    if A.dim() != 2 or Bt.dim() != 2:
+        raise ValueError(f"{name}: operands must be 2-D, got {A.dim()} and {Bt.dim()} dims")
+    M, K = A.shape
+    N, KB = (Bt.shape[0], Bt.shape[1]) if b_nk else (Bt.shape[1], Bt.shape[0])
+    if KB != K:
+        raise ValueError(f"{name}: K of A is {K}, of B {KB} (B {tuple(Bt.shape)})")
+    for tag, t in (("A", A), ("B", Bt)):
+        if t.dtype != torch.float64 or not t.is_contiguous() or not t.is_cuda or t.device != A.device:
+            raise ValueError(f"{name}: {tag} must be contiguous float64 on one GPU ({A.device})")
+    if out is not None and (tuple(out.shape) != (M, N) or out.dtype != torch.float64
+                            or not out.is_contiguous() or out.device != A.device):
+        raise ValueError(f"{name}: out must be contiguous float64 of shape {(M, N)} on {A.device}")
+    return M, N, K
+
+
 def mm_nt_events(A, Bt, primes, out, ws, events, exact=True, bits=53, use_corr=True):
     """fp64emu_mm_nt_events on preallocated `out` and workspace `ws`."""
     primes = np.ascontiguousarray(np.asarray(primes, dtype=np.int32))
-    M, K = A.shape
-    N = Bt.shape[1]
+    M, N, K = _check_nt("mm_nt_events", A, Bt, out)
+    if ws.dtype != torch.uint8 or not ws.is_contiguous() or ws.device != A.device:
+        raise ValueError(f"mm_nt_events: ws must be a contiguous uint8 tensor on {A.device}")
     _check(lib().fp64emu_mm_nt_events(out.data_ptr(), A.data_ptr(), Bt.data_ptr(), M, N, K,
                                       primes.ctypes.data_as(ctypes.c_void_p), None, None,
                                       primes.size, int(bool(exact)), int(bits),
@@ -241,12 +269,33 @@ def mm_nt_events(A, Bt, primes, out, ws, events, exact=True, bits=53, use_corr=T
     return out
 
 
+def bmm_nt_events(A, Bt, primes, out, ws, events, exact=True, bits=53, use_corr=True):
+    """fp64emu_bmm_nt_events on preallocated `out` [b, M, N] and workspace `ws`."""
+    primes = np.ascontiguousarray(np.asarray(primes, dtype=np.int32))
+    if A.dim() != 3 or Bt.dim() != 3 or Bt.shape[0] != A.shape[0] or Bt.shape[1] != A.shape[2]:
+        raise ValueError(f"bmm_nt_events: A {tuple(A.shape)} against Bt {tuple(Bt.shape)}")
+    batch, M, K = A.shape
+    N = Bt.shape[2]
+    for tag, t in (("A", A), ("Bt", Bt), ("out", out)):
+        if t.dtype != torch.float64 or not t.is_contiguous() or not t.is_cuda or t.device != A.device:
+            raise ValueError(f"bmm_nt_events: {tag} must be contiguous float64 on one GPU")
+    if tuple(out.shape) != (batch, M, N):
+        raise ValueError(f"bmm_nt_events: out must be of shape {(batch, M, N)}")
+    if ws.dtype != torch.uint8 or not ws.is_contiguous() or ws.device != A.device:
+        raise ValueError(f"bmm_nt_events: ws must be a contiguous uint8 tensor on {A.device}")
+    _check(lib().fp64emu_bmm_nt_events(out.data_ptr(), A.data_ptr(), Bt.data_ptr(), batch, M, N,
+                                       K, primes.ctypes.data_as(ctypes.c_void_p), None, None,
+                                       primes.size, int(bool(exact)), int(bits),
+                                       int(bool(use_corr)), ws.data_ptr(), ws.numel(),
+                                       _stream(), events.handles))
+    return out
+
+
 def mm_nt_noalloc(A, Bt, primes, out=None, exact=True, bits=53, use_corr=True):
     """fp64emu_mm_nt_noalloc: the library's static device scratch instead of
     a workspace argument."""
     primes = np.ascontiguousarray(np.asarray(primes, dtype=np.int32))
-    M, K = A.shape
-    N = Bt.shape[1]
+    M, N, K = _check_nt("mm_nt_noalloc", A, Bt, out)
     if out is None:
         out = torch.empty((M, N), dtype=torch.float64, device=A.device)
     _check(lib().fp64emu_mm_nt_noalloc(out.data_ptr(), A.data_ptr(), Bt.data_ptr(), M, N, K,
@@ -258,13 +307,83 @@ def mm_nt_noalloc(A, Bt, primes, out=None, exact=True, bits=53, use_corr=True):
 
 def ddgemm_nt(A, B):
     """Double-double C = A @ B^T on the device (A [M,K], B [N,K])."""
-    M, K = A.shape
-    N = B.shape[0]
+    M, N, K = _check_nt("ddgemm_nt", A, B, b_nk=True)
     hi = torch.empty((M, N), dtype=torch.float64, device=A.device)
     lo = torch.empty_like(hi)
     _check(lib().fp64emu_ddgemm_nt(hi.data_ptr(), lo.data_ptr(), A.data_ptr(), B.data_ptr(),
                                    M, N, K, _stream()))
     return hi, lo
+
+
+# ---- ceiling probes --------------------------------------------------------
+
+PROBE_SOURCE_BYTES = 2 * 2 * TILE_R * TILE_K   # two stages of an A and a B tile
+
+
+def probe_source(seed=0):
+    """The probe's two stages (host int8, 64 KiB): stage 0's A and B tiles
+    are random balanced residues in [-127, 127]; stage 1 holds the negated A
+    tile and the same B tile, so its products cancel stage 0's."""
+    rng = np.random.default_rng(seed)
+    tile = TILE_R * TILE_K
+    a = rng.integers(-127, 128, tile, dtype=np.int64).astype(np.int8)
+    b = rng.integers(-127, 128, tile, dtype=np.int64).astype(np.int8)
+    return np.concatenate([a, b, -a, b])
+
+
+def probe_expected(src):
+    """Group 0's accumulators after an odd step count (stage 0's products),
+    [4 waves, 8, 8, 256] int32, from the fragment order of the planes (lane
+    l = 16 (k / 16) + row holds k mod 16 as 16 bytes) and of the
+    accumulators (lane l's value v is row 4 (l / 16) + v, column l mod 16)."""
+    src = np.asarray(src, dtype=np.int8)
+    tile = TILE_R * TILE_K
+    lane = np.arange(64)
+    rows, kb = lane % 16, lane // 16
+
+    def frag(off):
+        F = src[off:off + FRAG].astype(np.int64).reshape(64, 16)
+        X = np.zeros((16, 64), np.int64)
+        for l in range(64):
+            X[rows[l], 16 * kb[l]:16 * kb[l] + 16] = F[l]
+        return X
+
+    out = np.zeros((4, 8, 8, 256), np.int64)
+    for w in range(4):
+        wm, wn = w >> 1, w & 1
+        for x in range(8):
+            Ax = frag((wm * 8 + x) * FRAG)
+            for y in range(8):
+                C = Ax @ frag(tile + (wn * 8 + y) * FRAG).T
+                for l in range(64):
+                    out[w, x, y, 4 * l:4 * l + 4] = C[4 * (l // 16):4 * (l // 16) + 4, l % 16]
+    return out.astype(np.int32)
+
+
+def probe_mfma(src_dev, groups, steps, mode):
+    """fp64emu_probe_mfma on a device int8 source of PROBE_SOURCE_BYTES.
+    Returns (acc [4, 8, 8, 256] int32, clocks [groups, 4] int64 device
+    tensors: clk0, clk1, rt0, rt1)."""
+    if src_dev.dtype != torch.int8 or src_dev.numel() != PROBE_SOURCE_BYTES or not src_dev.is_cuda:
+        raise ValueError(f"probe_mfma: source must be {PROBE_SOURCE_BYTES} int8 on a GPU")
+    acc = torch.empty((4, 8, 8, 256), dtype=torch.int32, device=src_dev.device)
+    clk = torch.empty((groups, 4), dtype=torch.int64, device=src_dev.device)
+    _check(lib().fp64emu_probe_mfma(acc.data_ptr(), clk.data_ptr(), src_dev.data_ptr(), groups,
+                                    steps, mode, _stream()))
+    return acc, clk
+
+
+def probe_stream(dst, src, mode):
+    """fp64emu_probe_stream over dst.numel() doubles (src: same size, unused
+    by mode 1)."""
+    n = dst.numel()
+    if dst.dtype != torch.float64 or not dst.is_contiguous() or not dst.is_cuda:
+        raise ValueError("probe_stream: dst must be contiguous float64 on a GPU")
+    if mode != 1 and (src is None or src.dtype != torch.float64 or src.numel() != n
+                      or not src.is_contiguous() or src.device != dst.device):
+        raise ValueError("probe_stream: src must match dst")
+    _check(lib().fp64emu_probe_stream(dst.data_ptr(), src.data_ptr() if src is not None else None,
+                                      n, mode, _stream()))
 
 
 # ---- workspace decoders (host, numpy) --------------------------------------

@@ -125,12 +125,24 @@ int fp64emu_mm_nt_events(double* out, const double* A, const double* Bt, int64_t
                          size_t workspace_bytes, fp64emu_stream_t stream,
                          const fp64emu_event_t* events /* host, 5 events */);
 
+/* fp64emu_bmm_nt with the phase events of fp64emu_mm_nt_events (the
+ * boundaries of the whole batch's launch chain).  No reference counterpart:
+ * the benchmark's per-phase times of batched configs. */
+int fp64emu_bmm_nt_events(double* out, const double* A, const double* Bt, int64_t batch, int64_t M,
+                          int64_t N, int64_t K, const int32_t* primes, const int32_t* inv,
+                          const int64_t* mu, int nprimes, int exact, int64_t bits, int use_corr,
+                          void* workspace, size_t workspace_bytes, fp64emu_stream_t stream,
+                          const fp64emu_event_t* events /* host, 5 events */);
+
 /* Bytes of the static device scratch of fp64emu_mm_nt_noalloc (64 MiB). */
 #define FP64EMU_NOALLOC_SCRATCH_BYTES (64ull << 20)
 
 /* fp64emu_mm_nt without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  No reference counterpart.  The
+ * first call on a device looks up the scratch's device address
+ * (hipGetSymbolAddress); a caller that captures should make one call on
+ * that device outside the capture first.  The
  * scratch is a static device array of FP64EMU_NOALLOC_SCRATCH_BYTES that the
  * library holds on every GPU it runs on until the process ends; the call
  * itself allocates nothing.  Products whose full workspace exceeds it run
@@ -210,6 +222,34 @@ int fp64emu_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int nprimes, 
  * (dd_matmul_nt), accumulating each dot product in ~106-bit arithmetic. */
 int fp64emu_ddgemm_nt(double* hi, double* lo, const double* A, const double* B, int64_t M,
                       int64_t N, int64_t K, fp64emu_stream_t stream);
+
+/* ---- Ceiling probes (measurement helpers, not on the product path; no
+ * reference counterpart).  They measure the rates this part attains, which
+ * the benchmark reports beside the datasheet peaks. ---- */
+
+/* The modular GEMM's inner loop, on `groups` work groups of 4 waves (one
+ * group per CU), `steps` steps of 64 v_mfma_i32_16x16x64_i8 per wave in the
+ * GEMM's order, over two 32 KiB stages of int8 fragments at `src` (64 KiB,
+ * A tile then B tile per stage, in the planes' fragment order).
+ *   mode 0: fragments held in registers (no memory traffic);
+ *   mode 1: the next step's fragments read from the GEMM's 4-stage LDS ring,
+ *           with its per-step wait and barrier;
+ *   mode 2: mode 1 plus the GEMM's global->LDS copies (from `src`, which the
+ *           L2 caches hold).
+ * acc_out (256 KiB) receives group 0's accumulators: the sum over the steps
+ * of each step's stage products, as [wave][x][y] blocks of 256 int32 (lane
+ * l's value v of the 16 x 16 block at 4 l + v: row 4 (l / 16) + v, column
+ * l % 16).  clocks[4 * g .. 4 * g + 3] receive group g's shader-clock counter
+ * (s_memtime) and 100 MHz real-time counter (s_memrealtime) at the start and
+ * the end of its loop: [clk0, clk1, rt0, rt1]. */
+int fp64emu_probe_mfma(int32_t* acc_out, unsigned long long* clocks, const int8_t* src,
+                       int64_t groups, int64_t steps, int mode, fp64emu_stream_t stream);
+
+/* HBM streaming over n doubles (n even, >= 2048; 16-byte aligned buffers):
+ * mode 0 reads src (the per-group sums go to dst[0 .. min(n / 2048, 4096))),
+ * mode 1 writes dst = 1.0 (src unused), mode 2 writes dst = -src. */
+int fp64emu_probe_stream(double* dst, const double* src, int64_t n, int mode,
+                         fp64emu_stream_t stream);
 
 #ifdef __cplusplus
 }

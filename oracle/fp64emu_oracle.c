@@ -234,8 +234,13 @@ int8_t or_residue(uint64_t uu, int p, int bits) {
 void or_extract_operand(const double* X, int64_t batch, int64_t R, int64_t K, int kn,
                         const int16_t* sft, int bits_eff, const int32_t* primes, int P,
                         int do_corr, int8_t* res, int8_t* hi, int8_t* q) {
-  for (int64_t b = 0; b < batch; b++)
-    for (int64_t r = 0; r < R; r++) {
+  /* Rows are independent (each element's split and residues depend on it
+   * and its row shift alone): OpenMP over rows. */
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+  for (int64_t br = 0; br < batch * R; br++) {
+      const int64_t b = br / R, r = br % R;
       const int s = sft[b * R + r];
       for (int64_t k = 0; k < K; k++) {
         const double x = kn ? X[(b * K + k) * R + r] : X[(b * R + r) * K + k];
@@ -382,6 +387,10 @@ static void or_reconstruct_any(const int8_t* res, const int32_t* c1, const int32
   or_tables(primes, P, minv, mppack, m64, &l2);
   const int cshift = bits_eff - 15;
   const int64_t total = M * N;
+  /* Elements are independent: OpenMP over rows. */
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
   for (int64_t i = 0; i < M; i++)
     for (int64_t j = 0; j < N; j++) {
       const int64_t idx = i * N + j;
@@ -591,6 +600,9 @@ void or_ddgemm_nt(double* hi, double* lo, const double* A, const double* Bt, int
 /* ---- array forms of the scalar restatements (for exhaustive pinning) ---- */
 
 void or_bal8_array(const int32_t* v, int64_t n, int p, int8_t* out) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
   for (int64_t i = 0; i < n; i++) out[i] = or_bal8(v[i], p);
 }
 

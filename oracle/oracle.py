@@ -291,6 +291,59 @@ def mm(A, B, b_kn, primes, exact=True, bits=53, use_corr=True, nthreads=0):
     return (out[0] if squeeze else out), info
 
 
+def int_gemm(A8, B8):
+    """Exact A8 @ B8^T of int8 planes A8 [M, K], B8 [N, K], as int64: one
+    float64 BLAS product (every partial sum, in any order, is an integer of
+    magnitude at most K * 128^2 < 2^53, so each operation is exact).  The
+    same integers as or_modgemm's sums, many times faster, for whole-output
+    checks at the benchmark sizes."""
+    A8, B8 = np.asarray(A8), np.asarray(B8)
+    assert A8.shape[1] * 128 * 128 < 2 ** 53
+    return (A8.astype(np.float64) @ B8.astype(np.float64).T).astype(np.int64)
+
+
+def mm_blas(A, B, b_kn, primes, exact=True, bits=53, use_corr=True):
+    """The whole pipeline of mm() (single launch depth, K <= 131071) with
+    the modular GEMMs as int_gemm products and the reference's bal8 on
+    their int32 sums: or_size_rows / or_size_cols / or_pick_bits,
+    or_extract_operand, int_gemm + or_bal8 (fp64_emu.cu:494-657),
+    or_reconstruct.  Bit-identical to mm() (the CPU tests check it);
+    returns (out, sizing dict)."""
+    A = _c(A, np.float64)
+    B = _c(B, np.float64)
+    squeeze = A.ndim == 2
+    if squeeze:
+        A, B = A[None], B[None]
+    batch, M, K = A.shape
+    if K > 131071:
+        raise ValueError("mm_blas: single-launch depth only (K <= 131071)")
+    N = B.shape[2] if b_kn else B.shape[1]
+    primes = _c(primes, np.int32)
+    P = primes.size
+    sA, lA = size_rows(A.reshape(-1, K), bits)
+    if b_kn:
+        sB, lB = size_cols(B, bits)
+    else:
+        sB, lB = size_rows(B.reshape(-1, K), bits)
+    _, _, _, log2M = tables(primes)
+    be, sA, sB = pick_bits(lA, lB, min(log2M, 126.0), bits, sA, sB)
+    out = np.zeros((batch, M, N), np.float64)
+    for b in range(batch):
+        rA, hA, qA = extract_operand(A[b:b + 1], 0, sA[b * M:(b + 1) * M], be, primes, use_corr)
+        rB, hB, qB = extract_operand(B[b:b + 1], 1 if b_kn else 0, sB[b * N:(b + 1) * N], be,
+                                     primes, use_corr)
+        res = np.zeros((P, M, N), np.int8)
+        for t in range(P):
+            res[t] = bal8_array(int_gemm(rA[0, t], rB[0, t]), int(primes[t]))
+        c1 = int_gemm(hA[0], qB[0]).astype(np.int32) if use_corr else None
+        c2 = int_gemm(qA[0], hB[0]).astype(np.int32) if use_corr else None
+        del rA, rB
+        out[b] = reconstruct(res, c1, c2, primes, be, sA[b * M:(b + 1) * M],
+                             sB[b * N:(b + 1) * N], exact)
+    info = dict(sftA=sA, sftB=sB, lgA=lA, lgB=lB, bits_eff=be)
+    return (out[0] if squeeze else out), info
+
+
 def ddgemm_nt(A, Bt, nthreads=0):
     """Double-double A [M,K] @ Bt [K,N] (bench/accuracy.py:21-50)."""
     A, Bt = _c(A, np.float64), _c(Bt, np.float64)

@@ -159,3 +159,27 @@ def sampled_parity(kind, A, B, primes, rows, cols, exact=True, bits=53, use_corr
     assert bits_equal(got, rec), "sampled outputs differ from the oracle"
     del Ah, Bh
     return out, gbe, lay, ws
+
+
+def whole_parity(kind, A, B, primes, exact=True, bits=53, use_corr=True):
+    """Parity of the whole output at the benchmark sizes: the C-ABI call on
+    a workspace filled with a nonzero byte, its sizing (shifts, width)
+    against the oracle's, and every output element bit for bit against the
+    oracle pipeline with BLAS modular products (O.mm_blas, which the CPU
+    tier pins to O.mm).  2-D kinds.  Returns (out, bits_eff, layout, ws)."""
+    b_kn = kind == "mm_nt"
+    out, ws, lay = capi.run(kind, A, B, primes, exact=exact, bits=bits, use_corr=use_corr,
+                            fill=0x5A)
+    torch.cuda.synchronize()
+    head = ws[:lay.off_planesA].cpu().numpy()
+    gsA, gsB, _, _, gbe = capi.sizing(head, lay)
+    Ah, Bh = A.cpu().numpy(), B.cpu().numpy()
+    oout, info = O.mm_blas(Ah, Bh, 1 if b_kn else 0, np.asarray(primes, dtype=np.int32),
+                           exact=exact, bits=bits, use_corr=use_corr)
+    assert info["bits_eff"] == gbe, f"bits_eff GPU {gbe} oracle {info['bits_eff']}"
+    assert np.array_equal(info["sftA"], gsA) and np.array_equal(info["sftB"], gsB), "shifts differ"
+    got = out.cpu().numpy()
+    same = got.view(np.uint64) == oout.view(np.uint64)
+    assert same.all(), f"{int((~same).sum())} of {same.size} outputs differ from the oracle"
+    del Ah, Bh, oout
+    return out, gbe, lay, ws

@@ -385,3 +385,45 @@ def test_baseline_config_launch_forms():
         L = capi.layout(*shape)
         got = (L.ksplit, L.gemm_tile_rows, L.gemm_tile_cols, L.gemm_run, L.ncorr, L.nslab)
         assert got == want, (name, got, want)
+
+
+def test_nt_helpers_check_operand_extents():
+    """mm_nt_events, mm_nt_noalloc and ddgemm_nt hand bare pointers to the
+    library: their ctypes helpers refuse mismatched shapes, dtypes, layouts
+    and host tensors before any call."""
+    A = torch.zeros(4, 5, dtype=torch.float64)
+    pr = capi_primes(3)
+    with pytest.raises(ValueError, match="K of A"):
+        capi.mm_nt_noalloc(A, torch.zeros(6, 3, dtype=torch.float64), pr)
+    with pytest.raises(ValueError, match="2-D"):
+        capi.mm_nt_noalloc(A, torch.zeros(1, 5, 3, dtype=torch.float64), pr)
+    with pytest.raises(ValueError, match="contiguous float64 on one GPU"):
+        capi.mm_nt_noalloc(A, torch.zeros(5, 3, dtype=torch.float64), pr)   # host tensors
+    with pytest.raises(ValueError, match="contiguous float64 on one GPU"):
+        capi.mm_nt_noalloc(A, torch.zeros(3, 5, dtype=torch.float64).t(), pr)
+    with pytest.raises(ValueError, match="K of A"):
+        capi.mm_nt_events(A, torch.zeros(4, 3, dtype=torch.float64), pr,
+                          torch.zeros(4, 3, dtype=torch.float64), None, None)
+    with pytest.raises(ValueError, match="K of A"):
+        capi.ddgemm_nt(A, torch.zeros(3, 6, dtype=torch.float64))
+
+
+def test_probe_source_and_expected_layout():
+    """The ceiling probe's source: balanced residues, stage 1 = (-A0, B0).
+    The expected accumulators decode the planes' fragment order and the
+    accumulator order: a single product of ones lands where they place it."""
+    src = capi.probe_source(1)
+    t = capi.TILE_R * capi.TILE_K
+    assert src.size == capi.PROBE_SOURCE_BYTES == 4 * t
+    assert src.min() >= -127 and src.max() <= 127
+    assert np.array_equal(src[2 * t:3 * t], -src[:t]) and np.array_equal(src[3 * t:], src[t:2 * t])
+    one = np.zeros(capi.PROBE_SOURCE_BYTES, np.int8)
+    # A fragment 0: row 5, k = 16 * 2 + 3 (lane 2 * 16 + 5, byte 3); B fragment
+    # 9 (wave wn = 1, y = 1): column 11, the same k (lane 2 * 16 + 11, byte 3).
+    one[16 * (2 * 16 + 5) + 3] = 3
+    one[t + 9 * capi.FRAG + 16 * (2 * 16 + 11) + 3] = -2
+    exp = capi.probe_expected(one)
+    nz = np.argwhere(exp)
+    # wave 1 (wm 0, wn 1), x 0, y 1; row 5 = 4 (l / 16) + v -> l / 16 = 1,
+    # v = 1; column 11 = l mod 16 -> lane 27, element 4 * 27 + 1.
+    assert nz.tolist() == [[1, 0, 1, 4 * 27 + 1]] and exp[1, 0, 1, 109] == -6

@@ -280,6 +280,8 @@ def test_concurrent_host_threads(dev):
         th.start()
     for th in threads:
         th.join(timeout=60)
+    hung = [i for i, th in enumerate(threads) if th.is_alive()]
+    assert not hung, f"threads {hung} ({[shapes[i] for i in hung]}) still running after 60 s"
     assert not errors, errors
     for t in range(len(inputs)):
         for r in range(3):

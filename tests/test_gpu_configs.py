@@ -3,9 +3,8 @@ inputs generated on the CPU from fixed seeds (1000*cfg, 1000*cfg + 1):
 
 - sizing (per-row/column shifts and the global width) bit-exact against the
   oracle on the full operands;
-- outputs at sampled rows and columns (always including the first and last,
-  where padding would leak) bit-exact against the oracle's pipeline on
-  those rows and columns;
+- every output element bit-exact against the oracle's pipeline (its modular
+  products as exact BLAS products, O.mm_blas, pinned to O.mm on the CPU);
 - correct bits against the device double-double GEMM at least native
   float64's (torch matmul on the same GPU);
 - the effective width within one bit of the values computed independently
@@ -20,7 +19,7 @@ import torch
 import fp64_emu as emu
 import oracle as O
 from fp64_emu import capi
-from parity_util import check_call, sampled_parity
+from parity_util import check_call, whole_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -56,7 +55,7 @@ def test_c2_square_8192(dev):
     Bt = torch.randn((n, n), dtype=torch.float64, generator=_gen(2001)).to(dev)
     P, corr = emu.plan_config(n)
     assert (P, corr) == (14, True)
-    out, be, lay, ws = sampled_parity("mm_nt", A, Bt, O.PRIMES[:P], _rows(n, 1), _rows(n, 2))
+    out, be, lay, ws = whole_parity("mm_nt", A, Bt, O.PRIMES[:P])
     del ws
     assert be == 49
     assert torch.equal(out, emu.mm_nt(A, Bt))
@@ -77,7 +76,7 @@ def test_c3a_wide_range_4096(dev):
     n = 4096
     A = _wide((n, n), _gen(3000)).to(dev)
     Bt = _wide((n, n), _gen(3001)).to(dev)
-    out, be, _, ws = sampled_parity("mm_nt", A, Bt, O.PRIMES[:14], _rows(n, 3), _rows(n, 4))
+    out, be, _, ws = whole_parity("mm_nt", A, Bt, O.PRIMES[:14])
     del ws
     assert abs(be - 50) <= 1
     emu_bits, nat_bits = _native_and_emu_bits(out, A, Bt)
@@ -93,7 +92,7 @@ def test_c3b_integer_exact_4096(dev):
     n = 4096
     A = torch.randint(-2 ** 20, 2 ** 20 + 1, (n, n), generator=_gen(3100)).double().to(dev)
     Bt = torch.randint(-2 ** 20, 2 ** 20 + 1, (n, n), generator=_gen(3101)).double().to(dev)
-    out, be, lay, ws = sampled_parity("mm_nt", A, Bt, O.PRIMES[:14], _rows(n, 5), _rows(n, 6))
+    out, be, lay, ws = whole_parity("mm_nt", A, Bt, O.PRIMES[:14])
     assert abs(be - 49) <= 1
     assert torch.equal(out, A @ Bt)
     rows = _rows(n, 7, 8)
@@ -127,8 +126,7 @@ def test_c5_ragged_deep_k(dev, P, corr):
     if corr:
         assert emu.plan_config(K) == (P, corr)
     expect_be = 51 if corr else 43
-    out, be, lay, ws = sampled_parity("mm_nt", A, Bt, O.PRIMES[:P], _rows(M, 8), _rows(N, 9),
-                                      use_corr=corr)
+    out, be, lay, ws = whole_parity("mm_nt", A, Bt, O.PRIMES[:P], use_corr=corr)
     del ws
     assert abs(be - expect_be) <= 1
     assert torch.equal(out, emu.mm_nt(A, Bt, nprimes=P, corr=corr))

@@ -269,3 +269,40 @@ def test_deep_k_segmentation_is_transparent():
     d2 = qA[0].astype(np.int64) @ hB[0].astype(np.int64).T
     rec = O.reconstruct64(res, d1, d2, pr, be, info["sftA"], info["sftB"])
     assert np.array_equal(out.view(np.uint64), rec.view(np.uint64))
+
+
+def test_int_gemm_is_exact_at_the_extremes():
+    """int_gemm stays exact at the largest sums: every entry
+    -128 over the deepest single launch (sum 131071 * 2^14 < 2^31), against
+    numpy int64 products, and random planes against or_modgemm's int32."""
+    A = np.full((3, 131071), -128, np.int8)
+    assert np.array_equal(O.int_gemm(A, A), np.full((3, 3), 131071 * 16384, np.int64))
+    rng = np.random.default_rng(5)
+    A = rng.integers(-128, 128, (41, 5000)).astype(np.int8)
+    B = rng.integers(-128, 128, (33, 5000)).astype(np.int8)
+    assert np.array_equal(O.int_gemm(A, B), A.astype(np.int64) @ B.astype(np.int64).T)
+    assert np.array_equal(O.int_gemm(A, B).astype(np.int32), O.modgemm(A, B, 0))
+
+
+@pytest.mark.parametrize("kind,shape,P,corr,exact", [
+    ("mm_nt", (1, 130, 70, 1500), 14, True, True),
+    ("mm", (1, 257, 129, 2049), 15, True, False),
+    ("bmm_nt", (3, 33, 65, 700), 13, False, True),
+    ("bmm", (2, 64, 31, 1025), 20, True, True),
+])
+def test_mm_blas_matches_mm(kind, shape, P, corr, exact):
+    """The whole-output checker of the full-size GPU configs (BLAS modular
+    products) is bit-identical to the oracle's pipeline on ragged, batched,
+    reduced and inexact cases, with rows spanning 2^-30 .. 2^30."""
+    batch, M, N, K = shape
+    rng = np.random.default_rng(M * N + K)
+    A = rng.standard_normal((batch, M, K)) * np.exp2(rng.integers(-30, 31, (batch, M, 1)))
+    b_kn = kind.endswith("_nt")
+    B = rng.standard_normal((batch, K, N) if b_kn else (batch, N, K))
+    if kind in ("mm", "mm_nt"):
+        A, B = A[0], B[0]
+    primes = O.PRIMES[:P]
+    ref, info = O.mm(A, B, int(b_kn), primes, exact=exact, use_corr=corr)
+    got, info2 = O.mm_blas(A, B, int(b_kn), primes, exact=exact, use_corr=corr)
+    assert info["bits_eff"] == info2["bits_eff"]
+    assert np.array_equal(ref.view(np.uint64), got.view(np.uint64))

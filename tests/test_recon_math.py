@@ -145,3 +145,51 @@ def test_branchless_conversion_matches_exact_rounding():
     for X in vals:
         hi, lo = X >> 64, X & ((1 << 64) - 1)
         assert _convert(hi, lo) == float(Fraction(X)), X
+
+
+def _fastdiv(d):
+    """make_fastdiv (fp64emu.hip): l = ceil(log2 d), m = floor(2^32 (2^l - d)
+    / d) + 1, as 32-bit words."""
+    d = max(int(d), 1)
+    l = 0
+    while (1 << l) < d:
+        l += 1
+    m = ((1 << 32) * ((1 << l) - d)) // d + 1
+    assert 0 < m < (1 << 32) or d == 1
+    return np.uint64(m & 0xFFFFFFFF), np.uint64(l)
+
+
+def _fastdiv_q(m, l, n):
+    """FastDiv::div in 32-bit words: (mulhi(m, n) + n) >> l, the add wrapping
+    like the kernel's uint32 arithmetic."""
+    s = (((m * n) >> np.uint64(32)) + n) & np.uint64(0xFFFFFFFF)
+    return s >> l
+
+
+def test_fastdiv_quotients():
+    """The round-up Granlund-Montgomery division that maps work-group indices
+    to (member, row group, k tile) and output blocks: q == n // d for every
+    divisor 1 .. 2^16 on sampled indices in [0, 2^24) (the 32-bit work-item
+    bound of a 256-thread launch) with each divisor's edge values, every
+    index below 2^24 for a few divisors, and random divisors up to 2^31 with
+    indices up to 2^31 - 1 (the range the kernel's sum stays below 2^32)."""
+    rng = np.random.default_rng(2024)
+    top = np.uint64(1 << 24)
+    sample = rng.integers(0, 1 << 24, 2048, dtype=np.uint64)
+    for d in range(1, (1 << 16) + 1):
+        m, l = _fastdiv(d)
+        du = np.uint64(d)
+        edges = np.array([0, 1, d - 1, d, d + 1, 2 * d - 1, 2 * d], dtype=np.uint64)
+        last = (top - np.uint64(1)) // du * du
+        edges = np.concatenate([edges, [last - np.uint64(1), last, top - np.uint64(1)]])
+        n = np.concatenate([sample, edges[edges < top]])
+        assert np.array_equal(_fastdiv_q(m, l, n), n // du), d
+    n = np.arange(1 << 24, dtype=np.uint64)
+    for d in (3, 7, 100, 641, 4095, 65537, 1 << 20, (1 << 24) - 1):
+        m, l = _fastdiv(d)
+        assert np.array_equal(_fastdiv_q(m, l, n), n // np.uint64(d)), d
+    big = rng.integers(0, 1 << 31, 4096, dtype=np.uint64)
+    big = np.concatenate([big, np.array([(1 << 31) - 1, (1 << 31) - 2], dtype=np.uint64)])
+    for d in np.concatenate([rng.integers(1 << 16, 1 << 31, 512), [(1 << 31) - 1, 1 << 30]]):
+        m, l = _fastdiv(int(d))
+        assert np.array_equal(_fastdiv_q(m, l, big), big // np.uint64(d)), int(d)

@@ -75,3 +75,33 @@ def test_noalloc_oracle_sample(dev):
     out, _, _, _ = sampled_parity("mm_nt", A, Bt, primes, rows=[0, 1, 255, 256, 1024, 1999],
                                   cols=[0, 5, 333, 499])
     assert torch.equal(got.view(torch.int64), out.view(torch.int64))
+
+
+def test_noalloc_under_graph_capture(dev):
+    """Callers under HIP graph capture: after one call on the device outside
+    any capture (it looks up the scratch's device address), a call of a
+    fresh shape is captured.  Each of three replays, with eager calls of
+    both entry points between them (the eager no-alloc call overwrites the
+    scratch), equals fp64emu_mm_nt bit for bit."""
+    primes = O.PRIMES[:14]
+    A0, B0 = _randn((64, 256), 830, dev), _randn((256, 48), 831, dev)
+    first = capi.mm_nt_noalloc(A0, B0, primes)
+    torch.cuda.synchronize()
+    M, N, K = 700, 300, 2500
+    print(f"case noalloc graph capture mm_nt {M}x{N}x{K}", flush=True)
+    A, Bt = _randn((M, K), 832, dev), _randn((K, N), 833, dev)
+    ref, _, _ = capi.run("mm_nt", A, Bt, primes)
+    out = torch.empty((M, N), dtype=torch.float64, device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        capi.mm_nt_noalloc(A, Bt, primes, out=out)
+    torch.cuda.synchronize()
+    for r in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int64), ref.view(torch.int64)), f"replay {r}"
+        again = capi.mm_nt_noalloc(A0, B0, primes)
+        capi.run("mm_nt", A0, B0, primes)
+        torch.cuda.synchronize()
+        assert torch.equal(again.view(torch.int64), first.view(torch.int64))
