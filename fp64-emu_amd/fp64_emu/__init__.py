@@ -1,15 +1,20 @@
-"""fp64_emu for MI355X: emulated FP64 GEMM on CDNA4 INT8 matrix cores (RARE).
+"""Double-precision matrix products on MI355X's INT8 matrix cores.
 
-C = A @ B is recovered from products modulo pairwise-coprime moduli (one
-INT8-MFMA GEMM each), combined by balanced-Garner reconstruction with a
-first-order quantization correction; a Cauchy-Schwarz sizing pass on the
-device keeps any modulus count range-safe.  Exactly representable integer
-products reproduce bit for bit.
+Each operand is scaled by powers of two, per row of A and per column of B,
+to integers of at most 53 bits.  Their product is then known exactly
+through its remainders modulo a list of small pairwise-coprime moduli, and
+each remainder costs one INT8 MFMA GEMM of balanced residues.  A mixed-radix
+(Garner) recombination of those remainders, plus two int8 GEMMs of the
+rounding residue that correct the scaling's first-order error, gives the
+float64 result.  How many moduli suffice is decided from K by the planner
+below, and a norm bound computed on the device narrows the integers until
+the product fits their range.  Integer inputs whose products are exact in
+float64 come out identical to the native product.
 
-Drop-in for the reference package torch-ext/fp64_emu/__init__.py: same
-functions, keywords, defaults and planner (line citations below).  The ops
-run on hand-written HIP kernels for gfx950; importing this package fails
-when the extension is not built.
+The functions, keywords, defaults and planner are those of the reference
+package (torch-ext/fp64_emu/__init__.py, cited line by line), so callers
+switch by import.  The work runs in hand-written gfx950 HIP kernels; without
+the built extension the import raises.
 """
 import math
 from functools import lru_cache
@@ -61,13 +66,19 @@ def _defaults(K, nprimes, corr):
 
 def mm(A: torch.Tensor, B: torch.Tensor, nprimes: int = None,
        exact: bool = True, bits: int = 53, corr: bool = None) -> torch.Tensor:
-    """Emulated FP64 C = A @ B with B given as [N, K]
+    """C = A @ B^T in float64 for A [M, K] and B [N, K]
     (torch-ext/fp64_emu/__init__.py:48-70).
 
-    nprimes: modulus count, one INT8 GEMM each; default by plan_config.
-    exact: 128-bit recombine (correctly rounded) vs fp64 recombine.
-    bits: mantissa width kept per operand; 53 keeps the full significand.
-    corr: the two cross GEMMs cancelling first-order quantization error.
+    nprimes: how many moduli, i.e. INT8 GEMMs; None lets plan_config(K)
+      choose.
+    exact: True recombines in 128-bit integers and rounds once; False
+      recombines in float64, slightly faster and a fraction of a bit less
+      accurate.
+    bits: the operands' integer width before the device narrows it; 53
+      keeps every bit of a float64 significand.
+    corr: whether to run the two INT8 GEMMs of the rounding residue that
+      remove the scaling's first-order error; None lets plan_config(K)
+      choose.
     """
     assert A.dim() == 2 and B.dim() == 2 and A.size(1) == B.size(1)
     M, K = A.shape
