@@ -2121,9 +2121,10 @@ reconstruct_kernel(ReconArgs a) {
   } else {
     // K-split: the S partial residues sum (|sum| <= 128 S) and fold to the
     // residue (any representative serves: each digit reduces mod p again),
-    // and the S x ncorr correction parts add up.  Two splits per iteration
-    // (S is a power of two >= 2), residues and corrections together, so the
-    // loads share each round trip.
+    // and the S x ncorr correction parts add up.  Two splits per iteration,
+    // residues and corrections together, so the loads share each round trip;
+    // for an odd S the last iteration's second split is zeros (a uniform
+    // condition), never a read past the S planes.
     int sums[kMaxP][4];
 #pragma unroll
     for (int t = 0; t < kMaxP; ++t)
@@ -2134,16 +2135,19 @@ reconstruct_kernel(ReconArgs a) {
       v4i cw[2][2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
+        const bool live = h == 0 || sp + 1 < a.ksplit;
 #pragma unroll
         for (int t = 0; t < kMaxP; ++t)
           if (t < P)
-            u[h][t] = *reinterpret_cast<const uint32_t*>(
-                a.res8 + (((sp + h) * a.batch + b) * P + t) * a.outplane + boff);
+            u[h][t] = live ? *reinterpret_cast<const uint32_t*>(
+                                 a.res8 + (((sp + h) * a.batch + b) * P + t) * a.outplane + boff)
+                           : 0u;
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc)
           if (cc < a.ncorr)
-            cw[h][cc] = *reinterpret_cast<const v4i*>(
-                a.corr + (((sp + h) * a.batch + b) * a.ncorr + cc) * a.outplane + boff);
+            cw[h][cc] = live ? *reinterpret_cast<const v4i*>(
+                                   a.corr + (((sp + h) * a.batch + b) * a.ncorr + cc) * a.outplane + boff)
+                             : v4i{0, 0, 0, 0};
       }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
