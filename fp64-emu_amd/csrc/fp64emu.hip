@@ -941,7 +941,7 @@ __device__ __forceinline__ uint32_t pack_bytes(int r0, int r1, int r2, int r3) {
   return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
-struct ExtractArgs {
+struct ExtractCore {
   const double* A;
   const double* B;
   int64_t M, N, K, batch;   // K: depth extracted by this launch (one segment)
@@ -968,15 +968,22 @@ struct ExtractArgs {
   int* bits_out;
   int8_t* planesA;
   int8_t* planesB;
-  ModTables tab;
+  int P;             // modulus count
 };
+
+// The kernels of the default modulus list take its constants at compile time
+// and no tables: a smaller kernel-argument block (about 1 KiB less), which a
+// dependent launch waits for (a 1 KiB block cost ~1.4 us per launch in a
+// back-to-back probe).  Any other list takes its tables by value.
+template <bool kTab> struct ExtractArgs : ExtractCore { ModTables tab; };
+template <> struct ExtractArgs<false> : ExtractCore {};
 
 // kDefault: the modulus list is a prefix of the default one, whose constants
 // the plane loop takes at compile time (no scalar load and wait per plane,
 // which dominated small launches); otherwise the tables of the arguments.
 template <bool kDefault>
 __global__ void __launch_bounds__(kThreads)
-extract_kernel(ExtractArgs a) {
+extract_kernel(ExtractArgs<!kDefault> a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   // The width pick, when this launch takes it: every wave reaches the
   // block's barrier before any returns.
@@ -1041,7 +1048,7 @@ extract_kernel(ExtractArgs a) {
 
   // A fragment that is all padding (its 16 rows or its 64 k past the
   // operand) only stores zeros: no loads and no residue arithmetic.
-  const int P = a.tab.P;
+  const int P = a.P;
   const int64_t nkt = a.nkt;
   const int64_t rt = rblk >> 4, fr = rblk & 15;
   const int64_t plane = isA ? a.planeA : a.planeB;
@@ -1129,9 +1136,13 @@ extract_kernel(ExtractArgs a) {
   // a tie's +p/2 into barrett_bal32's -p/2.  Each variant is its own copy
   // of the loop, so the usual moduli carry no extra compare.
   auto plane_residues = [&](auto int_path, auto tie_fix, int pi) {
-    const int pt = kDefault ? kDefaultTab.p[pi] : a.tab.p[pi];
-    const int c31 = kDefault ? kDefaultTab.c31[pi] : a.tab.c31[pi];
-    const double ip = kDefault ? kDefaultTab.invp[pi] : a.tab.invp[pi];
+    int pt, c31;
+    double ip;
+    if constexpr (kDefault) {
+      pt = kDefaultTab.p[pi]; c31 = kDefaultTab.c31[pi]; ip = kDefaultTab.invp[pi];
+    } else {
+      pt = a.tab.p[pi]; c31 = a.tab.c31[pi]; ip = a.tab.invp[pi];
+    }
     uint32_t w4[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -2025,7 +2036,7 @@ __device__ __forceinline__ double i128_to_f64(int64_t hi, uint64_t lo, int sh64)
   return ldexp(i64_to_f64((int64_t)top), sh64 - k);
 }
 
-struct ReconArgs {
+struct ReconCore {
   const int8_t* res8;
   const int32_t* corr;
   const int32_t* res32;   // K-segmented: residue sums, folded here
@@ -2042,8 +2053,13 @@ struct ReconArgs {
   FastDiv nbv_div;     // by NBv
   int ncorr;
   int ksplit;            // S: residue / correction planes per output, summed here
-  ModTables tab;
+  int P;                 // modulus count
 };
+
+// The modulus-count-specialised kernels (the default list) take their
+// constants at compile time and no tables, as the extraction's.
+template <bool kTab> struct ReconArgs : ReconCore { ModTables tab; };
+template <> struct ReconArgs<false> : ReconCore {};
 
 // kSplit: the GEMM ran with a K-split (its own instantiation, so the split
 // sums' registers do not weigh on the common path).  kP: the modulus count
@@ -2053,7 +2069,7 @@ struct ReconArgs {
 // kP = 0 handles any admissible list.
 template <bool kExact, bool kDeep, int kP, bool kSplit>
 __global__ void __launch_bounds__(kThreads)
-reconstruct_kernel(ReconArgs a) {
+reconstruct_kernel(ReconArgs<kP == 0> a) {
   // Block -> (member, 16-row block, 64-column block): uniform, so every
   // address below is a scalar base plus a 32-bit per-lane offset.
   const uint32_t blk = blockIdx.x;
@@ -2071,8 +2087,26 @@ reconstruct_kernel(ReconArgs a) {
   const int64_t rows_left = a.M - (int64_t)mb * 16;   // valid rows from the block's first
   if (j >= a.N || row0 >= rows_left) return;
 
-  const int P = kP > 0 ? kP : a.tab.P;
+  const int P = kP > 0 ? kP : a.P;
   constexpr bool kUsual = kP > 0;
+  // Table entries: compile-time constants of the default modulus list in
+  // the specialised kernels (no scalar registers held across the kernel and
+  // no tables among the arguments), kernel arguments otherwise.
+  auto tab_p = [&](int t) {
+    if constexpr (kUsual) return kDefaultTab.p[t]; else return a.tab.p[t];
+  };
+  auto tab_invp = [&](int t) {
+    if constexpr (kUsual) return kDefaultTab.invp[t]; else return a.tab.invp[t];
+  };
+  auto tab_nmp = [&](int i) {
+    if constexpr (kUsual) return kDefaultTab.nmp[i]; else return a.tab.nmp[i];
+  };
+  auto tab_mib = [&](int t) {
+    if constexpr (kUsual) return kDefaultTab.mib[t]; else return a.tab.mib[t];
+  };
+  auto tab_m64 = [&](int g) {
+    if constexpr (kUsual) return kDefaultM64[g]; else return a.tab.m64[g];
+  };
   // Byte (int8 planes) / element (int32 planes) offset of this block, and
   // the lane's offset inside it.
   const int64_t boff0 = ((int64_t)mb * a.NB + nb) * 1024;
@@ -2102,8 +2136,8 @@ reconstruct_kernel(ReconArgs a) {
         const int32_t* r = a.res32 + (b * P + t) * a.outplane + boff;
         v4i v = *reinterpret_cast<const v4i*>(r);
         for (int sp = 1; sp < a.ksplit; ++sp) v += *reinterpret_cast<const v4i*>(r + sp * sstride);
-        const double ip = a.tab.invp[t];
-        const int negp = -a.tab.p[t];
+        const double ip = tab_invp(t);
+        const int negp = -tab_p(t);
         w[t] = pack_bytes(acc_residue(v[0], ip, negp), acc_residue(v[1], ip, negp),
                           acc_residue(v[2], ip, negp), acc_residue(v[3], ip, negp));
       }
@@ -2169,7 +2203,7 @@ reconstruct_kernel(ReconArgs a) {
     for (int t = 0; t < kMaxP; ++t)
       if (t < P) {
         const int* sum4 = sums[t];
-        const double pd = (double)a.tab.p[t], ip = a.tab.invp[t];
+        const double pd = (double)tab_p(t), ip = tab_invp(t);
         uint32_t u = 0u;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -2191,13 +2225,6 @@ reconstruct_kernel(ReconArgs a) {
     }
   }
 
-  // Table entries: compile-time constants of the default modulus list in
-  // the specialised kernels (no scalar registers held across the kernel),
-  // kernel arguments otherwise.
-  auto tab_p = [&](int t) { return kUsual ? kDefaultTab.p[t] : a.tab.p[t]; };
-  auto tab_invp = [&](int t) { return kUsual ? kDefaultTab.invp[t] : a.tab.invp[t]; };
-  auto tab_nmp = [&](int i) { return kUsual ? kDefaultTab.nmp[i] : a.tab.nmp[i]; };
-  auto tab_mib = [&](int t) { return kUsual ? kDefaultTab.mib[t] : a.tab.mib[t]; };
 
   // Garner digits, 4 elements in lockstep.
   int dg[4][kMaxP];
@@ -2388,8 +2415,8 @@ reconstruct_kernel(ReconArgs a) {
       // mul_add_wide's four 32 x 32 -> 64 multiply-adds; longer lists take
       // the general 128-bit product (the true X stays below 2^127, so the
       // products wrap modulo 2^128 harmlessly).
-      const uint64_t m0 = kUsual ? (uint64_t)kDefaultM64[0] : (uint64_t)a.tab.m64[0];
-      const uint64_t m1 = kUsual ? (uint64_t)kDefaultM64[1] : (uint64_t)a.tab.m64[1];
+      const uint64_t m0 = (uint64_t)tab_m64(0);
+      const uint64_t m1 = (uint64_t)tab_m64(1);
       uint64_t lo;
       int64_t hi;
       if (ng == 1) {
@@ -2413,8 +2440,8 @@ reconstruct_kernel(ReconArgs a) {
       continue;
     } else {
       double acc = (double)(ng == 3 ? a2 : (ng == 2 ? a1 : a0));
-      if (ng == 3) acc = fma(acc, (double)a.tab.m64[1], (double)a1);
-      if (ng >= 2) acc = fma(acc, (double)a.tab.m64[0], (double)a0);
+      if (ng == 3) acc = fma(acc, (double)tab_m64(1), (double)a1);
+      if (ng >= 2) acc = fma(acc, (double)tab_m64(0), (double)a0);
       acc = acc + ldexp((double)cv[e], cshift);
       val = acc;
     }
@@ -2711,35 +2738,43 @@ int validate_primes(const int32_t* primes, int P) {
 // Modulus counts of the planner (plan_config: 14-15; plan: up to 20) get a
 // reconstruction compiled for their exact count; others use the generic one.
 template <bool kExact, bool kSplit>
-void launch_reconstruct_p(int P, unsigned grid, hipStream_t s, const ReconArgs& ra) {
-  // The specialised kernels carry the default modulus list's constants;
-  // other lists run the generic one.
+void launch_reconstruct_p(int P, unsigned grid, hipStream_t s, const ReconCore& rc,
+                          const ModTables& tab) {
+  // The specialised kernels carry the default modulus list's constants and
+  // take no tables; other lists run the generic one with the tables.
   bool usual = true;
-  for (int t = 0; t < P; ++t) usual = usual && ra.tab.p[t] == kDefaultModuli[t];
+  for (int t = 0; t < P; ++t) usual = usual && tab.p[t] == kDefaultModuli[t];
+  ReconArgs<false> rd;
+  static_cast<ReconCore&>(rd) = rc;
   switch (usual ? P : 0) {
 #define FP64EMU_RECON_CASE(n)                                                                   \
     case n:                                                                                     \
       hipLaunchKernelGGL((reconstruct_kernel<kExact, false, n, kSplit>), dim3(grid),            \
-                         dim3(kThreads), 0, s, ra);                                             \
+                         dim3(kThreads), 0, s, rd);                                             \
       return;
     FP64EMU_RECON_CASE(12) FP64EMU_RECON_CASE(13) FP64EMU_RECON_CASE(14)
     FP64EMU_RECON_CASE(15) FP64EMU_RECON_CASE(16) FP64EMU_RECON_CASE(17)
     FP64EMU_RECON_CASE(18) FP64EMU_RECON_CASE(19) FP64EMU_RECON_CASE(20)
 #undef FP64EMU_RECON_CASE
-    default:
+    default: {
+      ReconArgs<true> rg;
+      static_cast<ReconCore&>(rg) = rc;
+      rg.tab = tab;
       hipLaunchKernelGGL((reconstruct_kernel<kExact, false, 0, kSplit>), dim3(grid), dim3(kThreads),
-                         0, s, ra);
+                         0, s, rg);
+    }
   }
 }
 
-void launch_reconstruct(bool exact, int P, unsigned grid, hipStream_t s, const ReconArgs& ra) {
-  const bool split = ra.ksplit > 1;
+void launch_reconstruct(bool exact, int P, unsigned grid, hipStream_t s, const ReconCore& rc,
+                        const ModTables& tab) {
+  const bool split = rc.ksplit > 1;
   if (exact) {
-    if (split) launch_reconstruct_p<true, true>(P, grid, s, ra);
-    else launch_reconstruct_p<true, false>(P, grid, s, ra);
+    if (split) launch_reconstruct_p<true, true>(P, grid, s, rc, tab);
+    else launch_reconstruct_p<true, false>(P, grid, s, rc, tab);
   } else {
-    if (split) launch_reconstruct_p<false, true>(P, grid, s, ra);
-    else launch_reconstruct_p<false, false>(P, grid, s, ra);
+    if (split) launch_reconstruct_p<false, true>(P, grid, s, rc, tab);
+    else launch_reconstruct_p<false, false>(P, grid, s, rc, tab);
   }
 }
 
@@ -2920,7 +2955,7 @@ int run(const Call& c) {
       const int64_t k0 = (int64_t)seg * L.kseg;
       const int64_t kc = std::min<int64_t>(L.kseg, c.K - k0);
       const int64_t nkt = round_up(kc, kTileK) / kTileK;
-      ExtractArgs ea;
+      ExtractCore ea;
       ea.A = c.A + m0 * c.K; ea.B = c.B;
       ea.M = Mc; ea.N = c.N; ea.K = kc; ea.batch = c.batch;
       ea.lda = c.K; ea.k0 = k0;
@@ -2940,12 +2975,18 @@ int run(const Call& c) {
       ea.pick = pick_in_extract ? 1 : 0; ea.bits = c.bits; ea.log2M = log2M;
       ea.lgA = lgA; ea.lgB = lgB; ea.nlgA = MF; ea.nlgB = NF; ea.bits_out = bits_eff;
       ea.planesA = planesA; ea.planesB = planesB;
-      ea.tab = tab;
+      ea.P = c.P;
       const int64_t wg = c.batch * (ea.rgA + ea.rgB) * nkt;
-      if (default_moduli)
-        hipLaunchKernelGGL(extract_kernel<true>, dim3((unsigned)wg), dim3(kThreads), 0, s, ea);
-      else
-        hipLaunchKernelGGL(extract_kernel<false>, dim3((unsigned)wg), dim3(kThreads), 0, s, ea);
+      if (default_moduli) {
+        ExtractArgs<false> ed;
+        static_cast<ExtractCore&>(ed) = ea;
+        hipLaunchKernelGGL(extract_kernel<true>, dim3((unsigned)wg), dim3(kThreads), 0, s, ed);
+      } else {
+        ExtractArgs<true> eg;
+        static_cast<ExtractCore&>(eg) = ea;
+        eg.tab = tab;
+        hipLaunchKernelGGL(extract_kernel<false>, dim3((unsigned)wg), dim3(kThreads), 0, s, eg);
+      }
       if (c.ev) {
         if (int st = check_hip(hipEventRecord(c.ev[1], s), "hipEventRecord")) return st;
       }
@@ -2977,7 +3018,7 @@ int run(const Call& c) {
       if (int st = check_hip(hipEventRecord(c.ev[3], s), "hipEventRecord")) return st;
     }
 
-    ReconArgs ra;
+    ReconCore ra;
     ra.res8 = res8; ra.corr = corr;
     ra.res32 = reinterpret_cast<const int32_t*>(res8);
     ra.corr64 = reinterpret_cast<const int64_t*>(corr);
@@ -2991,15 +3032,18 @@ int run(const Call& c) {
     ra.nbv_div = make_fastdiv(ra.NBv);
     ra.ncorr = L.ncorr;
     ra.ksplit = L.ksplit;
-    ra.tab = tab;
+    ra.P = c.P;
     const unsigned grid = (unsigned)ra.nblocks;
     if (L.deep) {
+      ReconArgs<true> rg;
+      static_cast<ReconCore&>(rg) = ra;
+      rg.tab = tab;
       if (c.exact)
-        hipLaunchKernelGGL((reconstruct_kernel<true, true, 0, false>), dim3(grid), dim3(kThreads), 0, s, ra);
+        hipLaunchKernelGGL((reconstruct_kernel<true, true, 0, false>), dim3(grid), dim3(kThreads), 0, s, rg);
       else
-        hipLaunchKernelGGL((reconstruct_kernel<false, true, 0, false>), dim3(grid), dim3(kThreads), 0, s, ra);
+        hipLaunchKernelGGL((reconstruct_kernel<false, true, 0, false>), dim3(grid), dim3(kThreads), 0, s, rg);
     } else {
-      launch_reconstruct(c.exact, c.P, grid, s, ra);
+      launch_reconstruct(c.exact, c.P, grid, s, ra, tab);
     }
   }
   if (int st = check_hip(hipGetLastError(), "kernel launch")) return st;
