@@ -2,16 +2,21 @@
 the default plan, on one MI355X.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--n 8192] [--no-accuracy]
-                [--no-cpu] [--no-configs] [--configs [--config NAME]]
-                [--accuracy-grid] [--calibrate-copy]
+                [--no-cpu] [--no-configs] [--no-traffic] [--configs [--config NAME]]
+                [--accuracy-grid] [--bmm-sweep] [--square-sweep] [--card-grid]
+                [--small-n] [--first-call] [--ceilings] [--calibrate-copy]
 
 One step = one emulated mm_nt of resident 8192x8192 float64 operands (iid
 N(0,1) from CPU seeds 2000/2001, configs[1]) through the C ABI
 (fp64emu_mm_nt_events, workspace allocated once).  W untimed warm-up calls,
 then exactly K calls between two device synchronisations; value = 2 n^3 /
-(mean ms per call).  Prints one JSON line.  Besides the contract fields it
-reports: the per-phase ms (events recorded by each timed call at its phase
-boundaries), the same step through the torch op fp64_emu.mm_nt, native rocBLAS
+(mean ms per call; the median call's time beside it).  Prints one JSON line.
+Before the timing, two rocprofv3 --pmc child runs of this script count the
+GEMM launch's L2-boundary traffic (roofline.traffic).  Besides the contract
+fields it reports: the per-phase ms (events recorded by each timed call at its
+phase boundaries), the ceilings this part attains in the same run (the GEMM's
+MFMA loop with operands in registers, read from LDS, and fed by its copies;
+HBM streams), the same step through the torch op fp64_emu.mm_nt, native rocBLAS
 DGEMM (torch.matmul float64 on the device) throughput, correct bits of both
 against a device double-double GEMM, the plan-adjusted INT8 roofline
 fraction, the `roofline` object for the dominant kernel (the modular GEMM,
@@ -953,13 +958,13 @@ def cpu_torch_baseline(A, Bt):
 
 def cpu_baseline(A, Bt, P, corr):
     """The oracle port (the reference pipeline restated in C) on the host's
-    cores, on a bounded sample of the workload: the first 2048 rows of A and
+    cores, on a bounded sample of the workload: the first 4096 rows of A and
     columns of Bt at the full depth K, same plan (about 10 s on 16 cores).
-    Effective FP64 TFLOPS of that sample (2 * 2048 * 2048 * K / t)."""
+    Effective FP64 TFLOPS of that sample (2 * 4096 * 4096 * K / t)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     cores = _host_cores()
-    m = 2048
+    m = 4096
     a = A[:m].cpu().numpy()
     bt = Bt[:, :m].contiguous().cpu().numpy()
     K = a.shape[1]
