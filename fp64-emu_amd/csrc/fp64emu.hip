@@ -1263,6 +1263,19 @@ __device__ __forceinline__ void barrier_lds() {
 
 typedef __attribute__((address_space(3))) int8_t lds_i8;
 
+// Direct global->LDS copy of 16 bytes per lane: lane l's 16 bytes at g (its
+// own address) + kOff land at l (the wave's LDS base) + kOff + 16 l.  The
+// instruction's offset field is 13 bits, signed: the compiler encodes a
+// larger offset wrapped into the field without moving the address or M0
+// (4096 becomes -4096, so the copy reads 4 KiB before g: an out-of-bounds
+// read that faulted the GPU in a probe), so every copy keeps its offset in
+// [0, 4096) and larger steps advance the pointers instead.
+template <int kOff>
+__device__ __forceinline__ void copy_lds16(const int8_t* g, lds_i8* l) {
+  static_assert(kOff >= 0 && kOff < 4096, "global_load_lds: offset outside its 13-bit field");
+  __builtin_amdgcn_global_load_lds(g, l, 16, kOff, 0);
+}
+
 // One accumulator element read at its point of use.  With plain element
 // reads the compiler copies all 256 accumulators to VGPRs at the loop exit,
 // which overflows the VGPR file and spills; an AGPR operand keeps each value
@@ -1464,14 +1477,11 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   const int8_t* cpB = Bt;
 #define FP64EMU_SLOT(kt) ((kS == 4) ? ((kt) & 3) : ((kt) % kS))
 #define FP64EMU_COPY_A(kt, j)                                                               \
-  __builtin_amdgcn_global_load_lds((kRun ? cpA : At + (int64_t)(kt) * kTileBytes) + goff,   \
-                                   (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + wave * (kWM / 2) * 1024), \
-                                   16, (j) * 1024, 0)
+  copy_lds16<(j) * 1024>((kRun ? cpA : At + (int64_t)(kt) * kTileBytes) + goff,             \
+                         (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + wave * (kWM / 2) * 1024))
 #define FP64EMU_COPY_B(kt, j)                                                               \
-  __builtin_amdgcn_global_load_lds((kRun ? cpB : Bt + (int64_t)(kt) * kTileBytes) + goffB,  \
-                                   (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + kAB +           \
-                                             wave * (kWN / 2) * 1024),                      \
-                                   16, (j) * 1024, 0)
+  copy_lds16<(j) * 1024>((kRun ? cpB : Bt + (int64_t)(kt) * kTileBytes) + goffB,            \
+                         (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + kAB + wave * (kWN / 2) * 1024))
 #define FP64EMU_ISSUE(kt)                                                              \
   do {                                                                                 \
     FP64EMU_COPY_A(kt, 0);                                                             \
@@ -1562,7 +1572,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     const v4i* sa_ = reinterpret_cast<const v4i*>(lds + FP64EMU_SLOT((kt) + 1) * kSB);      \
     const v4i* sb_ = sa_ + kTileBytes / 16;                                                  \
     _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                          \
-      if (j == 0 && (c) <= 1) FP64EMU_COPY_A((kt) + kPF, (c) * 2);                             \
+      if (j == 0 && (c) <= 1) FP64EMU_COPY_A((kt) + kPF, (c) <= 1 ? (c) * 2 : 0);              \
       if (j == 2 && (c) == 0) FP64EMU_COPY_A((kt) + kPF, 1);                                   \
       if (j == 0 && (c) == 2) FP64EMU_COPY_A((kt) + kPF, 3);                                   \
       if (j == 2 && (c) == 2) FP64EMU_COPY_B((kt) + kPF, 0);                                   \
@@ -2603,11 +2613,10 @@ mfma_probe_kernel(const int8_t* __restrict__ src, int64_t steps, int32_t* __rest
       for (int j = 0; j < 4; ++j) {
         if constexpr (kMode == 2) {
           const int half = (c >> 1) * kTileBytes;   // chunks 0, 1 copy A; 2, 3 copy B
-          // (The builtin's offset must be a literal.)
-          if (j == 0 && !(c & 1)) __builtin_amdgcn_global_load_lds(cg + half, cl + half, 16, 0, 0);
-          if (j == 2 && !(c & 1)) __builtin_amdgcn_global_load_lds(cg + half, cl + half, 16, 1024, 0);
-          if (j == 0 && (c & 1)) __builtin_amdgcn_global_load_lds(cg + half, cl + half, 16, 2048, 0);
-          if (j == 2 && (c & 1)) __builtin_amdgcn_global_load_lds(cg + half, cl + half, 16, 3072, 0);
+          if (j == 0 && !(c & 1)) copy_lds16<0>(cg + half, cl + half);
+          if (j == 2 && !(c & 1)) copy_lds16<1024>(cg + half, cl + half);
+          if (j == 0 && (c & 1)) copy_lds16<2048>(cg + half, cl + half);
+          if (j == 2 && (c & 1)) copy_lds16<3072>(cg + half, cl + half);
         }
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (kMode != 0) {
