@@ -262,6 +262,17 @@ void slab_split(int64_t NF, int64_t K, int64_t* kslab, int* nslab) {
 // splits 0.292 ms, 8 splits 0.281 ms).  A function of the shapes only, so
 // the workspace size is too.
 constexpr int kCUs = 256;
+// Item streams: items per work group (see stream_order), for items of more
+// than kRunMaxSteps and at most kStreamMaxSteps k-steps.  Measured against
+// one item per group, whole calls in one process: 4096^2 x 2560 0.784 ->
+// 0.766 ms, 4096^2 x 3072 0.900 -> 0.873, 3000^3 0.554 -> 0.537, 4096^3
+// 1.120 -> 1.100 at 8 items per group (2 and 4 gained less); even at
+// 6144^2 x 3072, 6144^2 x 4096 and 8192^2 x 4096; slower from 80 k-steps
+// (5120^3 2.02 -> 2.05, 4096^2 x 8192 2.017 -> 2.04, 8192^3 7.14 -> 7.30 at
+// 2 items, 7.45 at one group per CU), where the GEMM runs at the part's
+// power limit and the time between items is no longer what bounds it.
+constexpr int kStreamChain = 8;
+constexpr int64_t kStreamMaxSteps = 64;
 constexpr int kMaxSplit = 16;
 
 int choose_ksplit(int64_t batch, int64_t tiles, int64_t nkt, int P, int ncorr, int64_t out_elems,
@@ -1237,6 +1248,7 @@ struct GemmArgs {
   int ksplit;          // groups per output tile, each over a contiguous K range
   int run;             // residue slots per run group (1: one slot per group)
   int corr_run;        // 1: each tile's run starts with the (fused) correction slot
+  int chain;           // item streams: items per work group
   int p[kMaxP];
   double invp[kMaxP];
 };
@@ -1400,6 +1412,35 @@ __device__ __forceinline__ GemmItem gemm_item(const GemmArgs& g) {
   return it;
 }
 
+// Item streams (one slot per item, no K-split): work group gq runs the
+// items q = 256 g.chain (gq / 256) + 256 j + gq % 256, j < g.chain (those
+// below g.total).  Item q is the item that group q of the one-item-per-group
+// launch takes (gemm_item), so the chip works through the items in the same
+// order and XCD placement (group gq runs on XCD gq % 8, as group q would),
+// and the hardware still balances the CUs, group by group.
+__device__ __forceinline__ uint32_t stream_order(const GemmArgs& g, uint32_t q) {
+  return (q >> 8) < (uint32_t)(g.total >> 8) ? (q & ~255u) + (q & 7) * 32 + ((q & 255) >> 3) : q;
+}
+
+__device__ __forceinline__ GemmItem stream_item(const GemmArgs& g, uint32_t L) {
+  const uint32_t tiles = (uint32_t)(g.TM * g.TN);
+  const uint32_t sb = L / tiles;                      // (slot, member)
+  const uint32_t tile = L - sb * tiles;
+  GemmItem it;
+  it.split = 0;
+  it.nrun = 1;
+  it.slot = (int)(sb / (uint32_t)g.batch);
+  it.b = sb - (uint32_t)it.slot * (uint32_t)g.batch;
+  const uint32_t GM = 8, TM = (uint32_t)g.TM;
+  const uint32_t grp = tile / (GM * (uint32_t)g.TN);
+  const uint32_t first_m = grp * GM;
+  const uint32_t gm = min(TM - first_m, GM);
+  const uint32_t within = tile - grp * GM * (uint32_t)g.TN;
+  it.mt = (int)(first_m + within % gm);
+  it.nt = (int)(within / gm);
+  return it;
+}
+
 // Balanced residues of one 16 x 64 output block of the accumulators (row
 // block x, column block h of this wave's tile) to `dst` (16 bytes per lane),
 // for slot runs.  Stage by stage over the block's 16 values, so that no
@@ -1425,7 +1466,7 @@ __device__ __forceinline__ void store_residue_block(const v4i (&acc)[kWM][kWN], 
 // One output tile of one slot (kRun: of it.nrun consecutive residue slots):
 // the body of the GEMM kernels, on the group's LDS ring `lds` (the kernel's
 // single LDS object).
-template <bool kDeep, int kWM, int kWN, bool kRun = false>
+template <bool kDeep, int kWM, int kWN, bool kRun = false, bool kStream = false>
 __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, const GemmItem it) {
   using Sh = GemmShape<kWM, kWN>;
   constexpr int kSB = Sh::kSB, kDma = Sh::kDma, kHB = Sh::kHB;
@@ -1471,16 +1512,17 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   // the LDS address alike.
   const uint32_t goff = (uint32_t)(wave * (kWM / 2) * 1024 + lane * 16);
   const uint32_t goffB = (uint32_t)(wave * (kWN / 2) * 1024 + lane * 16);
-  // kRun: the source tiles of the stage being copied, set before its copies
-  // (the k-step stream crosses from one slot's planes to the next).
+  // kRun, kStream: the source tiles of the stage being copied, set before its
+  // copies (the k-step stream crosses from one slot's planes, or one item's
+  // tiles, to the next).
   const int8_t* cpA = At;
   const int8_t* cpB = Bt;
 #define FP64EMU_SLOT(kt) ((kS == 4) ? ((kt) & 3) : ((kt) % kS))
 #define FP64EMU_COPY_A(kt, j)                                                               \
-  copy_lds16<(j) * 1024>((kRun ? cpA : At + (int64_t)(kt) * kTileBytes) + goff,             \
+  copy_lds16<(j) * 1024>((kRun || kStream ? cpA : At + (int64_t)(kt) * kTileBytes) + goff,   \
                          (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + wave * (kWM / 2) * 1024))
 #define FP64EMU_COPY_B(kt, j)                                                               \
-  copy_lds16<(j) * 1024>((kRun ? cpB : Bt + (int64_t)(kt) * kTileBytes) + goffB,            \
+  copy_lds16<(j) * 1024>((kRun || kStream ? cpB : Bt + (int64_t)(kt) * kTileBytes) + goffB,  \
                          (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + kAB + wave * (kWN / 2) * 1024))
 #define FP64EMU_ISSUE(kt)                                                              \
   do {                                                                                 \
@@ -1518,6 +1560,10 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
 #define FP64EMU_STEP(kt, FC, FN, MMA)                                                    \
   do {                                                                                   \
     if ((kt) + kPF <= nk) wait_vm_lgkm0<(kPF - 2) * kDma>(); else wait_vm_lgkm0<0>();     \
+    FP64EMU_STEP_BODY(kt, FC, FN, MMA);                                                  \
+  } while (0)
+#define FP64EMU_STEP_BODY(kt, FC, FN, MMA)                                               \
+  do {                                                                                   \
     barrier_lds();                                                                       \
     if ((kt) + kPF < nk) FP64EMU_ISSUE((kt) + kPF);                                      \
     FP64EMU_READF(FN, (kt) + 1);                                                         \
@@ -1628,6 +1674,56 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   // holds kWM row blocks x kWN/4 column blocks.  Element 16 l + 4 q + v of a
   // block is lane l's value v of accumulator column block q (row
   // 4 (l / 16) + v, column 16 q + l % 16).
+  // Streams (kRun, kStream): k-step G of the group's stream of nk k-steps,
+  // whose copy (stage G + kPF) exists while G + kPF < nk; next_src() sets the
+  // copy sources of the next stage.
+#define FP64EMU_RSTEP(G, FC, FN, MMA)                                                       \
+  do {                                                                                      \
+    if ((G) + kPF < nk) next_src();                                                         \
+    FP64EMU_STEP(G, FC, FN, MMA);                                                           \
+  } while (0)
+#define FP64EMU_RSTEP_FULL(G, FC, FN)                                                       \
+  do {                                                                                      \
+    next_src();                                                                             \
+    FP64EMU_STEP_FULL(G, FC, FN, mma16);                                                    \
+  } while (0)
+  // The first k-step G0 of a slot (or item) leaves the previous one's stores
+  // in flight: the stage it waits for (G0 + 1) was copied at step G0 - 2, and
+  // the copies of stage G0 + 2 (step G0 - 1) and then the stores were issued
+  // after it, so at most kRelax younger operations outstanding proves that
+  // it landed, by the in-order retirement below; the stores retire during
+  // that step instead of stalling its start.  (A correction slot stores four
+  // times as many: a larger margin.  A stream's first slot follows the
+  // prologue, which waited for everything.)
+  constexpr int kRelax = (kPF - 2) * kDma + kWM * kHB;
+  static_assert(kRelax < 64, "vmcnt field");
+#define FP64EMU_RSTEP_R(G, FC, FN, MMA)                                                     \
+  do {                                                                                      \
+    if ((G) + kPF < nk) next_src();                                                         \
+    if ((G) + kPF <= nk) wait_vm_lgkm0<kRelax>(); else wait_vm_lgkm0<0>();                  \
+    FP64EMU_STEP_BODY(G, FC, FN, MMA);                                                      \
+  } while (0)
+  // One slot (or item) of a stream: k-steps G0 .. G0 + nj - 1, its first
+  // stage landed and visible (the wait and barrier of the stream's previous
+  // step, or the prologue's), no copy targeting it before its first step.
+#define FP64EMU_STREAM_SLOT(G0, nj)                                                         \
+  do {                                                                                      \
+    v4i F0[kWM + kWN], F1[kWM + kWN];                                                       \
+    FP64EMU_READF(F0, (G0));                                                                \
+    FP64EMU_RSTEP_R((G0), F0, F1, mma16_init);                                              \
+    int kt_ = 1;                                                                            \
+    const int kf_ = nk - kPF - (G0);   /* steps kt_ < kf_ copy stage G0 + kt_ + kPF */      \
+    for (; kt_ + 2 <= (nj) && kt_ + 1 < kf_; kt_ += 2) {                                    \
+      FP64EMU_RSTEP_FULL((G0) + kt_, F1, F0);                                               \
+      FP64EMU_RSTEP_FULL((G0) + kt_ + 1, F0, F1);                                           \
+    }                                                                                       \
+    for (; kt_ + 2 <= (nj); kt_ += 2) {                                                     \
+      FP64EMU_RSTEP((G0) + kt_, F1, F0, mma16);                                             \
+      FP64EMU_RSTEP((G0) + kt_ + 1, F0, F1, mma16);                                         \
+    }                                                                                       \
+    if (kt_ < (nj)) FP64EMU_RSTEP((G0) + kt_, F1, F0, mma16);                               \
+    mfma_fence();                                                                           \
+  } while (0)
   if constexpr (kRun) {
     const int64_t NB = g.NB;
     const int64_t rb0 = (int64_t)mt * (2 * kWM) + wm * kWM, cb0 = (int64_t)nt * (kWN / 2) + wn * kHB;
@@ -1653,18 +1749,23 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     const int8_t* ArA = crun ? g.A + b * g.memberA + (int64_t)mrt * g.nkt * kTileBytes : At;
     const int8_t* ArB = crun ? g.B + b * g.memberB + (int64_t)nrt * g.nkt * kTileBytes : Bt;
     const int nkr = nkc + (it.nrun - (crun ? 1 : 0)) * nks;
-    // The next stage to copy: residue slot cj of the run (-1: the correction
-    // slot), k-step ckt.
-    int cj = crun ? -1 : 0, ckt = 0;
+    // The copy side: the next stage's sources nA, nB, in residue slot cj of
+    // the run (-1: the correction slot), cleft stages left in that slot.
+    // The step advances two pointers; a slot crossing (rare) moves them to
+    // the next plane.
+    int cj = crun ? -1 : 0, cleft = crun ? nkc : nks;
+    const int8_t* nA = crun ? At : ArA;
+    const int8_t* nB = crun ? Bt : ArB;
     auto next_src = [&]() {
-      if (cj < 0) {
-        cpA = At + (int64_t)ckt * kTileBytes;
-        cpB = Bt + (int64_t)ckt * kTileBytes;
-        if (++ckt == nkc) { ckt = 0; cj = 0; }
-      } else {
-        cpA = ArA + (int64_t)cj * g.planeA + (int64_t)ckt * kTileBytes;
-        cpB = ArB + (int64_t)cj * g.planeB + (int64_t)ckt * kTileBytes;
-        if (++ckt == nks) { ckt = 0; ++cj; }
+      cpA = nA;
+      cpB = nB;
+      nA += kTileBytes;
+      nB += kTileBytes;
+      if (__builtin_expect(--cleft == 0, 0)) {
+        ++cj;
+        nA = ArA + (int64_t)cj * g.planeA;
+        nB = ArB + (int64_t)cj * g.planeB;
+        cleft = nks;
       }
     };
     auto store_corr = [&]() {
@@ -1697,52 +1798,108 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     };
     {
       const int nk = nkr;   // the STEP macros' end of stream
-      // A k-step G of the stream; its copy (stage G + kPF) exists while G + kPF < nk.
-#define FP64EMU_RSTEP(G, FC, FN, MMA)                                                       \
-  do {                                                                                      \
-    if ((G) + kPF < nk) next_src();                                                         \
-    FP64EMU_STEP(G, FC, FN, MMA);                                                           \
-  } while (0)
-#define FP64EMU_RSTEP_FULL(G, FC, FN)                                                       \
-  do {                                                                                      \
-    next_src();                                                                             \
-    FP64EMU_STEP_FULL(G, FC, FN, mma16);                                                    \
-  } while (0)
 #pragma unroll
       for (int s = 0; s < kPF; ++s)
         if (s < nk) { next_src(); FP64EMU_ISSUE(s); }
       wait_vm_lgkm0<0>();
       barrier_lds();
       for (int j = 0; j < it.nrun; ++j) {
-        // Slot j: k-steps G0 .. G0 + nj - 1.  Its first stage has landed
-        // and is visible (the wait and barrier of the stream's previous
-        // step), and no copy targets it before this slot's first step.
+        // Slot j of the run.
         const bool jc = crun && j == 0;
         const int nj = jc ? nkc : nks;
         const int G0 = jc ? 0 : nkc + (j - (crun ? 1 : 0)) * nks;
-        v4i F0[kWM + kWN], F1[kWM + kWN];
-        FP64EMU_READF(F0, G0);
-        FP64EMU_RSTEP(G0, F0, F1, mma16_init);
-        int kt = 1;
-        const int kf = nk - kPF - G0;   // steps kt < kf copy stage G0 + kt + kPF
-        for (; kt + 2 <= nj && kt + 1 < kf; kt += 2) {
-          FP64EMU_RSTEP_FULL(G0 + kt, F1, F0);
-          FP64EMU_RSTEP_FULL(G0 + kt + 1, F0, F1);
-        }
-        for (; kt + 2 <= nj; kt += 2) {
-          FP64EMU_RSTEP(G0 + kt, F1, F0, mma16);
-          FP64EMU_RSTEP(G0 + kt + 1, F0, F1, mma16);
-        }
-        if (kt < nj) FP64EMU_RSTEP(G0 + kt, F1, F0, mma16);
-        mfma_fence();
+        FP64EMU_STREAM_SLOT(G0, nj);
         if (jc) store_corr();
         else store_slot(slot + j);
       }
-#undef FP64EMU_RSTEP
-#undef FP64EMU_RSTEP_FULL
       // No copy or store may still be in flight when the group retires.
       wait_vm_lgkm0<0>();
     }
+  } else if constexpr (kStream) {
+    // Item stream (256 x 256 tiles, no K-split): the group runs its items
+    // (stream_order, stream_item) as one stream of k-steps, the copies
+    // running ahead across item boundaries as a run's do across slots, so
+    // that an item's first stages land while the previous item ends and
+    // stores its outputs, and no item waits on its own group's launch and
+    // prologue.
+    const uint32_t q0 = (blockIdx.x >> 8) * (uint32_t)(256 * g.chain) + (blockIdx.x & 255);
+    if (q0 >= g.total) return;   // the last groups of a partial last round
+    const int nitems = (int)min<int64_t>(g.chain, (g.total - q0 + 255) / 256);
+    // Items below corr_end (in launch order) are correction slots: csteps
+    // k-steps each (the fused pair: twice a residue slot's).
+    const uint32_t corr_end = (uint32_t)(g.ncorr * g.batch) * (uint32_t)(g.TM * g.TN);
+    const int csteps = g.ncorr == 1 ? 2 * g.nkt : g.nkt;
+    int nk = 0;
+    for (int j = 0; j < nitems; ++j)
+      nk += stream_order(g, q0 + (uint32_t)j * 256) < corr_end ? csteps : g.nkt;
+    // The copy side: the next stage's sources nA, nB, in item cj, cleft
+    // stages left in that item.  The step advances two pointers; an item
+    // crossing (rare) decodes the next item.
+    int cj = 0, cleft = 0;
+    const int8_t* nA = nullptr;
+    const int8_t* nB = nullptr;
+    auto copy_item = [&](const int j) {
+      const GemmItem t = stream_item(g, stream_order(g, q0 + (uint32_t)j * 256));
+      const bool ic = t.slot < g.ncorr;
+      const int pl = ic ? g.P : t.slot - g.ncorr;
+      const int rs = ic ? 2 * g.nkt : g.nkt;                       // k tiles per row tile
+      const int k0 = (ic && g.ncorr == 2) ? t.slot * g.nkt : 0;
+      nA = g.A + t.b * g.memberA + (int64_t)pl * g.planeA + ((int64_t)t.mt * rs + k0) * kTileBytes;
+      nB = g.B + t.b * g.memberB + (int64_t)pl * g.planeB + ((int64_t)t.nt * rs + k0) * kTileBytes;
+      cleft = ic ? csteps : g.nkt;
+    };
+    copy_item(0);
+    auto next_src = [&]() {
+      cpA = nA;
+      cpB = nB;
+      nA += kTileBytes;
+      nB += kTileBytes;
+      if (__builtin_expect(--cleft == 0, 0) && cj + 1 < nitems) copy_item(++cj);
+    };
+    const int64_t NB = g.NB;
+#pragma unroll
+    for (int s = 0; s < kPF; ++s)
+      if (s < nk) { next_src(); FP64EMU_ISSUE(s); }
+    wait_vm_lgkm0<0>();
+    barrier_lds();
+    int G0 = 0;
+    for (int j = 0; j < nitems; ++j) {
+      const GemmItem t = stream_item(g, stream_order(g, q0 + (uint32_t)j * 256));
+      const bool ic = t.slot < g.ncorr;
+      const int nj = ic ? csteps : g.nkt;
+      FP64EMU_STREAM_SLOT(G0, nj);
+      const int64_t rb0 = (int64_t)t.mt * (2 * kWM) + wm * kWM, cb0 = (int64_t)t.nt * (kWN / 2) + wn * kHB;
+      if (ic) {
+        int32_t* cdst = g.corr + (t.b * g.ncorr + t.slot) * g.outplane;
+#pragma unroll
+        for (int x = 0; x < kWM; ++x)
+#pragma unroll
+          for (int h = 0; h < kHB; ++h) {
+            v4i* d = reinterpret_cast<v4i*>(cdst + ((rb0 + x) * NB + cb0 + h) * 1024 + lane * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              d[q] = v4i{acc_read(acc[x][4 * h + q][0]), acc_read(acc[x][4 * h + q][1]),
+                         acc_read(acc[x][4 * h + q][2]), acc_read(acc[x][4 * h + q][3])};
+            __builtin_amdgcn_sched_barrier(0);
+          }
+      } else {
+        const int tp = t.slot - g.ncorr;
+        const double ip = g.invp[tp];
+        const int negp = -g.p[tp];
+        int8_t* rdst = g.res8 + (t.b * g.P + tp) * g.outplane;
+#pragma unroll
+        for (int x = 0; x < kWM; ++x)
+#pragma unroll
+          for (int h = 0; h < kHB; ++h) {
+            store_residue_block<kWM, kWN>(acc, x, h, ip, negp,
+                                          rdst + ((rb0 + x) * NB + cb0 + h) * 1024 + lane * 16);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+      }
+      G0 += nj;
+    }
+    // No copy or store may still be in flight when the group retires.
+    wait_vm_lgkm0<0>();
   } else if (nk == 0) {
     // A trailing K-split group past the end: its outputs are zeros.
 #pragma unroll
@@ -1783,11 +1940,16 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
 #undef FP64EMU_READF
 #undef FP64EMU_MMA
 #undef FP64EMU_STEP
+#undef FP64EMU_STEP_BODY
 #undef FP64EMU_CHUNK
 #undef FP64EMU_CHUNK_W
 #undef FP64EMU_CHUNK_N
 #undef FP64EMU_CHUNK_S
 #undef FP64EMU_STEP_FULL
+#undef FP64EMU_RSTEP
+#undef FP64EMU_RSTEP_FULL
+#undef FP64EMU_RSTEP_R
+#undef FP64EMU_STREAM_SLOT
 #undef FP64EMU_COPY_A
 #undef FP64EMU_COPY_B
 #undef FP64EMU_SLOT
@@ -1795,7 +1957,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   // Epilogue (of a single slot; a run stores each slot as it ends).
   const int64_t NB = g.NB;
   const int64_t rb0 = (int64_t)mt * (2 * kWM) + wm * kWM, cb0 = (int64_t)nt * (kWN / 2) + wn * kHB;
-  if constexpr (kRun) {
+  if constexpr (kRun || kStream) {
   } else if (kDeep && is_corr) {
     // K-segmented: this segment's correction products join the int64 sum.
     typedef long long v2l __attribute__((ext_vector_type(2)));
@@ -1893,12 +2055,17 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   }
 }
 
-template <bool kDeep, int kWM, int kWN, bool kRun = false>
+template <bool kDeep, int kWM, int kWN, bool kRun = false, bool kStream = false>
 __global__ void __launch_bounds__(kThreads, (kWM == 8 && kWN == 8) ? 1 : 2)
 modgemm_kernel(GemmArgs g) {
-  static_assert(!kRun || (kWM == 8 && kWN == 8), "slot runs: 256 x 256 tiles only");
+  static_assert(!(kRun || kStream) || (kWM == 8 && kWN == 8 && !kDeep),
+                "slot runs and item streams: 256 x 256 tiles only");
   using Sh = GemmShape<kWM, kWN>;
   __shared__ __attribute__((aligned(1024))) int8_t lds[Sh::kLdsBytes];
+  if constexpr (kStream) {
+    modgemm_tile<false, kWM, kWN, false, true>(g, lds, GemmItem{});
+    return;
+  }
   const GemmItem it = gemm_item(g);
   if constexpr (kRun) {
     if (it.nrun > 1) {
@@ -2887,6 +3054,12 @@ int run(const Call& c) {
   // Work items per tile: the correction slots, then the residue slots in runs.
   const int64_t vslots = ga.corr_run ? 1 : L.ncorr + (c.P + ga.run - 1) / ga.run;
   ga.total = vslots * c.batch * L.ksplit * ga.TM * ga.TN;
+  // 256 x 256 tiles one slot per item of at most kStreamMaxSteps k-steps, no
+  // K-split, at least two items per CU: groups of kStreamChain items, each
+  // run as one stream (modgemm_tile's kStream), instead of one group per item.
+  const bool stream = !L.deep && ga.run == 1 && !narrow && !mixed && L.ksplit == 1 &&
+                      ga.total >= 2 * kCUs && L.Kp / kTileK <= kStreamMaxSteps;
+  ga.chain = kStreamChain;
 
   {
     // A dispatch holds its grid size in work-items as 32 bits: every launch
@@ -2900,7 +3073,8 @@ int run(const Call& c) {
     const int64_t sizing =
         !c.b_kn ? (MF + NF < kRowsGroupBelow ? MF + NF : (MF + NF + kRowsPerBlock - 1) / kRowsPerBlock)
         : kslab <= kFusedSlabRows
-            ? ((group ? (MF + 3) / 4 : (MF + 15) / 16) +
+            ? ((group ? (MF + kSizeThreads / 256 - 1) / (kSizeThreads / 256)
+                      : (MF + kSizeThreads / 64 - 1) / (kSizeThreads / 64)) +
                (NF + kSizeThreads / nslab - 1) / (kSizeThreads / nslab)) * (kSizeThreads / kThreads)
             : (group ? MF : (MF + kRowsPerBlock - 1) / kRowsPerBlock) + (NF + kThreads - 1) / kThreads * nslab;
     const int64_t extraction = c.batch * (L.ext_rowsA / 64 + L.ext_rowsB / 64) * (L.Kp / kTileK);
@@ -3011,6 +3185,10 @@ int run(const Call& c) {
         hipLaunchKernelGGL((modgemm_kernel<false, 8, 4>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       else if (mixed)
         hipLaunchKernelGGL(modgemm_mixed_kernel, dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+      else if (stream)   // groups of ga.chain items, each run as one stream
+        hipLaunchKernelGGL((modgemm_kernel<false, 8, 8, false, true>),
+                           dim3((unsigned)((ga.total + 256 * ga.chain - 1) / (256 * ga.chain) * 256)),
+                           dim3(kThreads), 0, s, ga);
       else
         hipLaunchKernelGGL((modgemm_kernel<false, 8, 8>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       for (int t = 0; t < c.P && !L.deep; ++t) {

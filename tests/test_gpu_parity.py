@@ -513,3 +513,47 @@ def test_deep_slot_runs_sampled(dev):
     rows = [0, 255, 256, n - 1] + list(rng.integers(0, n, 12))
     cols = [0, 255, 256, n - 1] + list(rng.integers(0, n, 12))
     sampled_parity("mm_nt", A, Bt, O.PRIMES[:14], rows, cols)
+
+
+def _item_stream(L, N):
+    """The GEMM launch runs work groups of several items, each over its items
+    as one stream (256 x 256 tiles, one slot per item of at most 64 k-steps,
+    no K-split, at least 512 items)."""
+    Np = -(-N // 256) * 256
+    mixed = Np // 256 >= 2 and N % 256 != 0 and N % 256 <= 128
+    items = (L.nprimes + L.ncorr) * L.batch * (L.chunk_rows // 256) * (Np // 256)
+    return (not L.deep and L.gemm_run == 1 and L.ksplit == 1 and not mixed
+            and (L.gemm_tile_rows, L.gemm_tile_cols) == (256, 256) and items >= 512
+            and -(-L.K // 64) <= 64)
+
+
+STREAM_CASES = [
+    # kind, batch, M, N, K, moduli, corr -- items (tiles x slots) in the comment.
+    ("mm", 1, 2304, 2560, 3000, O.PRIMES[:14], True),     # 1350: five whole rounds and 70
+    ("bmm", 3, 1024, 1024, 2500, MODULI_ORDERS[1], True),  # 720, even modulus 254
+    ("bmm_nt", 2, 1536, 1792, 2100, O.PRIMES[:13], False), # 1092, no correction slot
+    ("mm_nt", 1, 2048, 2048, 2200, O.PRIMES[:20], True),  # 1344, every modulus
+    ("mm_nt", 1, 3072, 2048, 4096, O.PRIMES[:14], True),  # 1440, 64 k-steps (the limit)
+]
+
+
+@pytest.mark.parametrize("kind,batch,M,N,K,primes,corr", STREAM_CASES)
+def test_item_stream_parity(dev, kind, batch, M, N, K, primes, corr):
+    """Products of many 256 x 256 tiles at 33 to 64 k-steps per slot run the
+    GEMM in work groups of eight items, each over its items as one stream of
+    operand copies (the items of a group in different tiles, slots and
+    members; correction items twice as deep; the last groups with fewer
+    items): every stage against the oracle."""
+    from fp64_emu import capi
+    P = len(primes)
+    print(f"case item stream {kind} b={batch} {M}x{N}x{K} P={P} corr={corr}", flush=True)
+    assert _item_stream(capi.layout(batch, M, N, K, P, corr), N)
+    seed = 3700 + batch + M + N + K + P
+    if kind in ("bmm", "bmm_nt"):
+        A = _randn((batch, M, K), seed, dev)
+        B = _randn((batch, K, N) if kind == "bmm_nt" else (batch, N, K), seed + 1, dev)
+    else:
+        A = _randn((M, K), seed, dev)
+        B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
+    check_call(kind, A, B, primes, use_corr=corr)
+
