@@ -816,9 +816,18 @@ def run_configs(steps, warmup, names, emit=True):
         def timed(fn):
             # At least `steps` calls and about 50 ms of them (small configs
             # take tens of microseconds, where a handful of calls would time
-            # mostly the host's synchronisation).
-            for _ in range(warmup):
+            # mostly the host's synchronisation), after at least `warmup`
+            # calls and about 100 ms of them: each config follows seconds of
+            # host-side input generation with the GPU idle, and a shorter
+            # warm-up timed the clock's ramp (c3a: 1.142 ms per call against
+            # 1.051 ms summed over its phases in the same run).
+            t0 = time.perf_counter()
+            i = 0
+            while i < warmup or time.perf_counter() - t0 < 0.1:
                 fn()
+                i += 1
+                if i % 8 == 0:
+                    torch.cuda.synchronize()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             fn()
