@@ -144,7 +144,8 @@ def test_deep_k_parity(dev, kind, batch, M, N, K, P, corr, exact):
 
 @pytest.mark.parametrize("kind,M,N,K", [("mm_nt", 1000, 700, 3000), ("mm", 777, 300, 1500),
                                         ("mm_nt", 2000, 100, 4096),
-                                        ("mm_nt", 1300, 900, 700)])   # shallow: slot runs
+                                        ("mm_nt", 1300, 900, 700),    # shallow: slot runs
+                                        ("mm_nt", 4096, 2048, 3000)])  # item streams (full run)
 def test_row_chunks_match_full(dev, kind, M, N, K):
     """A workspace below the full size runs the rows of A in chunks against
     one extraction of B; the output is bit-identical to the full run, at
