@@ -558,3 +558,41 @@ def test_item_stream_parity(dev, kind, batch, M, N, K, primes, corr):
         B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
     check_call(kind, A, B, primes, use_corr=corr)
 
+
+
+def test_item_stream_random_whole_parity(dev):
+    """Eight seeded random products that take the item stream (mm and mm_nt,
+    12 to 20 moduli, with and without the correction, exact and fp64
+    combines; normal, wide-range and integer entries): every output element
+    bit for bit against the oracle pipeline (BLAS modular products)."""
+    from fp64_emu import capi
+    from parity_util import whole_parity
+    rng = np.random.default_rng(4711)
+    done = 0
+    while done < 8:
+        kind = str(rng.choice(["mm", "mm_nt"]))
+        M, N = (int(x) for x in rng.integers(1300, 3400, 2))
+        K = int(rng.integers(2060, 4097))
+        P = int(rng.integers(12, 21))
+        corr, exact = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+        dist = int(rng.integers(0, 3))
+        seed = int(rng.integers(1 << 30))
+        if not _item_stream(capi.layout(1, M, N, K, P, corr), N):
+            continue
+        print(f"case random item stream {kind} {M}x{N}x{K} P={P} corr={corr} exact={exact} "
+              f"dist={dist}", flush=True)
+        g = torch.Generator().manual_seed(seed)
+
+        def gen(shape):
+            if dist == 0:
+                return torch.randn(shape, dtype=torch.float64, generator=g)
+            if dist == 1:
+                s = torch.randint(0, 2, shape, generator=g) * 2 - 1
+                m = 1 + torch.rand(shape, generator=g, dtype=torch.float64)
+                return s * torch.ldexp(m, torch.randint(-30, 31, shape, generator=g))
+            return torch.randint(-2 ** 20, 2 ** 20 + 1, shape, generator=g).double()
+        A = gen((M, K)).to(dev)
+        B = gen((K, N) if kind == "mm_nt" else (N, K)).to(dev)
+        whole_parity(kind, A, B, O.PRIMES[:P], exact=exact, use_corr=corr)
+        done += 1
+        del A, B
