@@ -228,6 +228,12 @@ def measure_traffic(n, timeout=240):
     if not os.path.exists(prof):
         log("traffic: rocprofv3 not found")
         return None
+    # Under a profiler the children would inherit its preloaded tool library,
+    # which opens the GPU in every process of the child's launch chain
+    # before that chain execs the next program: skip the measurement.
+    if "rocprofiler" in os.environ.get("LD_PRELOAD", "") or "ROCP_TOOL_LIBRARIES" in os.environ:
+        log("traffic: skipped (this run is itself under rocprofv3)")
+        return None
     res = {}
     env = dict(os.environ, TMPDIR="/tmp")
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
