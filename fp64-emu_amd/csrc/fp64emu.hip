@@ -377,6 +377,40 @@ int slot_run_length(const fp64emu_layout_t& L) {
   return r >= 2 ? r : 1;
 }
 
+// Split streams: a deep product of 256 x 256 tiles for which the planner
+// chose a K-split runs one work group per CU instead of rounds of split
+// groups.  Its units are the K-deep (tile, slot) products (the correction
+// products as two slots) in stream_item's order, in blocks of 32 units (a
+// block of tiles sharing their operand panels).  XCD x's 32 groups walk the
+// x-th eighth of the blocks' k-steps, group j taking unit j of each block:
+// the XCD's groups run the same k-steps of one block together, sharing its
+// panels in that XCD's L2, and every XCD has the same number of k-steps.
+// With at least eight blocks an eighth spans at least one block, so a unit
+// falls into at most two K ranges (stored as the two planes of a K-split of
+// 2).  The K-split's rounds leave their last round partly empty (1088
+// groups of 256 k-steps on 256 CUs: 5 rounds for 4.25 of work), though the
+// part then runs its busy CUs at a higher clock, so that measured whole
+// calls, one process, against the K-split: 1024 x 2048 x 32768 1.576 ->
+// 1.520 ms, 1024^2 x 32768 (K-split 4) 1.009 -> 0.969, 1024 x 2048 x 16384
+// 0.851 -> 0.830, 4 x 512 x 1024 x 16384 batched 1.176 -> 1.168.  Only
+// where that was measured to gain: units of at least kSplitMinSteps k-steps
+// (1024^2 x 8192: 0.273 -> 0.280 ms, 1024^2 x 4096: 0.150 -> 0.162, where
+// the groups' stores at their common end are exposed), and tile counts per
+// member and slot that divide or are divided by 32, so that a block's tiles
+// belong to one slot (36 and 48 tiles: 1500^2 x 30000 1.501 -> 1.534 ms,
+// 3000 x 1000 x 20000 1.364 -> 1.374).  Not with a last tile column of at
+// most 128 columns (the mixed launch's half-width tiles).
+constexpr int64_t kSplitMinSteps = 256;
+bool use_split_streams(const fp64emu_layout_t& L) {
+  if (L.deep || L.nchunk != 1 || L.ksplit < 2 || use_narrow_gemm(L)) return false;
+  if (L.Np / kTileR >= 2 && L.N % kTileR != 0 && L.N % kTileR <= 128) return false;
+  if (L.Kp / kTileK < kSplitMinSteps) return false;
+  const int64_t tiles = (L.Mp / kTileR) * (L.Np / kTileR);
+  if (tiles % 32 != 0 && 32 % tiles != 0) return false;
+  const int64_t units = (int64_t)(L.nprimes + (L.use_corr ? 2 : 0)) * L.batch * tiles;
+  return (units + 31) / 32 >= 8;
+}
+
 // nchunk_req > 1 (batch 1, not K-segmented): the planes of A and the output
 // planes hold one chunk of ceil(TM / nchunk_req) row tiles at a time.
 void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool corr,
@@ -416,6 +450,10 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   // (two int32 planes): a fused 2K-deep slot would make its groups twice as
   // long as every residue group (choose_ksplit already counts it as two).
   if (L->ksplit > 1 && L->ncorr == 1) L->ncorr = 2;
+  if (use_split_streams(*L)) {
+    L->gemm_split = 1;
+    L->ksplit = 2;
+  }
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o = align_up(o + bytes); return at; };
   L->off_sftA = take(sizeof(int16_t) * batch * M);
@@ -432,7 +470,7 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   L->off_corr = take((L->deep ? sizeof(int64_t) : sizeof(int32_t)) *
                      (size_t)(L->ksplit * batch * L->ncorr * L->outplane_bytes));
   L->total = o;
-  L->gemm_tile_cols = use_narrow_gemm(*L) ? 128 : 256;
+  L->gemm_tile_cols = (!L->gemm_split && use_narrow_gemm(*L)) ? 128 : 256;
   // 128 x 128 tiles where 128-row tiles also cut the padded work by > 10%
   // (M <= 128: half): two groups per CU, a quarter of the 256 x 256 work.
   const int64_t rows128 = (std::max<int64_t>(M, 1) + 127) / 128 * 128;
@@ -1465,8 +1503,9 @@ __device__ __forceinline__ void store_residue_block(const v4i (&acc)[kWM][kWN], 
 
 // One output tile of one slot (kRun: of it.nrun consecutive residue slots):
 // the body of the GEMM kernels, on the group's LDS ring `lds` (the kernel's
-// single LDS object).
-template <bool kDeep, int kWM, int kWN, bool kRun = false, bool kStream = false>
+// single LDS object).  kStream: an item stream; with kSplitS, a split stream.
+template <bool kDeep, int kWM, int kWN, bool kRun = false, bool kStream = false,
+          bool kSplitS = false>
 __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, const GemmItem it) {
   using Sh = GemmShape<kWM, kWN>;
   constexpr int kSB = Sh::kSB, kDma = Sh::kDma, kHB = Sh::kHB;
@@ -1815,6 +1854,115 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
       // No copy or store may still be in flight when the group retires.
       wait_vm_lgkm0<0>();
     }
+  } else if constexpr (kSplitS) {
+    // Split stream (use_split_streams): one group per CU, group j = blockIdx.x
+    // / 8 of XCD x = blockIdx.x % 8.  The g.total units (stream_item order) form
+    // nblk blocks of 32 of g.nkt k-steps each; XCD x's share is block-steps
+    // [x Tb / 8, (x + 1) Tb / 8) of the Tb = nblk g.nkt, and group j runs
+    // unit 32 bl + j of each block bl in it, the pieces (one block's k range
+    // each) as one stream of k-steps whose copies run ahead across pieces.
+    // A piece starting at k-step 0 stores its sums as split 0, else as split
+    // 1; a piece covering its unit whole also stores zeros as split 1.
+    const int x = (int)(blockIdx.x & 7u);
+    const uint32_t jl = blockIdx.x >> 3;
+    const uint32_t U = (uint32_t)g.total;
+    const uint32_t nblk = (U + 31u) >> 5;
+    const int64_t Tb = (int64_t)nblk * g.nkt;
+    const int64_t s0 = (int64_t)x * Tb / 8;
+    int64_t e0 = (int64_t)(x + 1) * Tb / 8;
+    // The last block holds U - 32 (nblk - 1) units: later groups stop before it.
+    if (jl >= U - 32u * (nblk - 1u)) e0 = min(e0, (int64_t)(nblk - 1u) * g.nkt);
+    if (s0 >= e0) return;
+    const int nk = (int)(e0 - s0);
+    const uint32_t bfirst = (uint32_t)(s0 / g.nkt);          // the first piece's block
+    const int kfirst = (int)(s0 - (int64_t)bfirst * g.nkt);  // and its first k-step
+    uint32_t cbl = bfirst;                                   // block of the copy side's piece
+    // The copy side: the next stage's sources nA, nB, cleft stages left in
+    // the piece; a piece crossing moves to k-step 0 of the next block's unit.
+    int cleft = 0;
+    const int8_t* nA = nullptr;
+    const int8_t* nB = nullptr;
+    int64_t cend = e0 - (int64_t)cbl * g.nkt;               // stream end, from the piece's block
+    auto copy_piece = [&](const int k) {
+      const GemmItem t = stream_item(g, cbl * 32u + jl);
+      const bool ic = t.slot < g.ncorr;                     // ncorr is 2 (or 0) here
+      const int pl = ic ? g.P : t.slot - g.ncorr;
+      const int rs = ic ? 2 * g.nkt : g.nkt;                // k tiles per row tile
+      const int k0 = (ic ? t.slot * g.nkt : 0) + k;
+      nA = g.A + t.b * g.memberA + (int64_t)pl * g.planeA + ((int64_t)t.mt * rs + k0) * kTileBytes;
+      nB = g.B + t.b * g.memberB + (int64_t)pl * g.planeB + ((int64_t)t.nt * rs + k0) * kTileBytes;
+      cleft = (int)min<int64_t>(g.nkt, cend) - k;
+    };
+    copy_piece(kfirst);
+    auto next_src = [&]() {
+      cpA = nA;
+      cpB = nB;
+      nA += kTileBytes;
+      nB += kTileBytes;
+      if (__builtin_expect(--cleft == 0, 0) && cend > g.nkt) {
+        ++cbl;
+        cend -= g.nkt;
+        copy_piece(0);
+      }
+    };
+    const int64_t NB = g.NB;
+#pragma unroll
+    for (int s = 0; s < kPF; ++s)
+      if (s < nk) { next_src(); FP64EMU_ISSUE(s); }
+    wait_vm_lgkm0<0>();
+    barrier_lds();
+    int G0 = 0;
+    uint32_t bl = bfirst;
+    int k0 = kfirst;
+    while (G0 < nk) {
+      const int nj = min(g.nkt - k0, nk - G0);
+      FP64EMU_STREAM_SLOT(G0, nj);
+      const GemmItem t = stream_item(g, bl * 32u + jl);
+      const bool whole = k0 == 0 && nj == g.nkt;
+      const int64_t sbm = (int64_t)(k0 == 0 ? 0 : 1) * g.batch + t.b;   // split-major planes
+      const int64_t rb0 = (int64_t)t.mt * (2 * kWM) + wm * kWM, cb0 = (int64_t)t.nt * (kWN / 2) + wn * kHB;
+      if (t.slot < g.ncorr) {
+        int32_t* cdst = g.corr + (sbm * g.ncorr + t.slot) * g.outplane;
+        const int64_t zoff = (int64_t)g.batch * g.ncorr * g.outplane;   // split 1, in int32s
+#pragma unroll
+        for (int x_ = 0; x_ < kWM; ++x_)
+#pragma unroll
+          for (int h = 0; h < kHB; ++h) {
+            int32_t* c = cdst + ((rb0 + x_) * NB + cb0 + h) * 1024 + lane * 16;
+            v4i* d = reinterpret_cast<v4i*>(c);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              d[q] = v4i{acc_read(acc[x_][4 * h + q][0]), acc_read(acc[x_][4 * h + q][1]),
+                         acc_read(acc[x_][4 * h + q][2]), acc_read(acc[x_][4 * h + q][3])};
+            if (whole) {
+              v4i* z = reinterpret_cast<v4i*>(c + zoff);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) z[q] = v4i{0, 0, 0, 0};
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+      } else {
+        const int tp = t.slot - g.ncorr;
+        const double ip = g.invp[tp];
+        const int negp = -g.p[tp];
+        int8_t* rdst = g.res8 + (sbm * g.P + tp) * g.outplane;
+        const int64_t zoff = (int64_t)g.batch * g.P * g.outplane;        // split 1
+#pragma unroll
+        for (int x_ = 0; x_ < kWM; ++x_)
+#pragma unroll
+          for (int h = 0; h < kHB; ++h) {
+            int8_t* d = rdst + ((rb0 + x_) * NB + cb0 + h) * 1024 + lane * 16;
+            store_residue_block<kWM, kWN>(acc, x_, h, ip, negp, d);
+            if (whole) *reinterpret_cast<v4i*>(d + zoff) = v4i{0, 0, 0, 0};
+            __builtin_amdgcn_sched_barrier(0);
+          }
+      }
+      G0 += nj;
+      ++bl;
+      k0 = 0;
+    }
+    // No copy or store may still be in flight when the group retires.
+    wait_vm_lgkm0<0>();
   } else if constexpr (kStream) {
     // Item stream (256 x 256 tiles, no K-split): the group runs its items
     // (stream_order, stream_item) as one stream of k-steps, the copies
@@ -2089,6 +2237,14 @@ modgemm_mixed_kernel(GemmArgs g) {
   } else {
     modgemm_tile<false, 8, 8>(g, lds, it);
   }
+}
+
+// Split streams (use_split_streams): 256 groups, one per CU, each running
+// its share of the units' k-steps as one stream (modgemm_tile's kSplitS).
+__global__ void __launch_bounds__(kThreads, 1)
+modgemm_split_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) int8_t lds[GemmShape<8, 8>::kLdsBytes];
+  modgemm_tile<false, 8, 8, false, true, true>(g, lds, GemmItem{});
 }
 
 // ---------------------------------------------------------------------------
@@ -3054,6 +3210,9 @@ int run(const Call& c) {
   // Work items per tile: the correction slots, then the residue slots in runs.
   const int64_t vslots = ga.corr_run ? 1 : L.ncorr + (c.P + ga.run - 1) / ga.run;
   ga.total = vslots * c.batch * L.ksplit * ga.TM * ga.TN;
+  // Split streams: g.total counts the K-deep units (the correction products
+  // as two slots: ncorr is 2), which 256 groups share.
+  if (L.gemm_split) ga.total = (int64_t)ga.nslots * c.batch * ga.TM * ga.TN;
   // 256 x 256 tiles one slot per item of at most kStreamMaxSteps k-steps, no
   // K-split, at least two items per CU: groups of kStreamChain items, each
   // run as one stream (modgemm_tile's kStream), instead of one group per item.
@@ -3177,6 +3336,8 @@ int run(const Call& c) {
       ga.first = seg == 0 ? 1 : 0;
       if (L.deep)
         hipLaunchKernelGGL((modgemm_kernel<true, 8, 8>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
+      else if (L.gemm_split)   // 256 x 256 tiles, K-split 2 (use_split_streams)
+        hipLaunchKernelGGL(modgemm_split_kernel, dim3(kCUs), dim3(kThreads), 0, s, ga);
       else if (ga.run > 1)   // 256 x 256 tiles only (use_slot_runs)
         hipLaunchKernelGGL((modgemm_kernel<false, 8, 8, true>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
       else if (small)

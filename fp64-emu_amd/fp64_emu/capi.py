@@ -44,7 +44,7 @@ class Layout(ctypes.Structure):
                        "off_pss", "off_planesA", "off_planesB", "off_res8", "off_corr", "total")] + [
                    ("gemm_tile_cols", ctypes.c_int), ("gemm_tile_rows", ctypes.c_int),
                    ("gemm_run", ctypes.c_int), ("ext_rowsA", ctypes.c_int64),
-                   ("ext_rowsB", ctypes.c_int64)]
+                   ("ext_rowsB", ctypes.c_int64), ("gemm_split", ctypes.c_int)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}

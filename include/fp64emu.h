@@ -211,6 +211,14 @@ typedef struct {
                                that GEMM tiles read (a multiple of 128, at most the padded
                                row count); rows past it hold unspecified bytes */
   int64_t ext_rowsB;        /* the same for B's plane rows (the columns of B^T) */
+  int gemm_split;           /* 1: the modular GEMM runs as split streams (one work group
+                               per CU; each XCD's 32 groups walk an equal share of the
+                               K-deep (tile, slot) units in blocks of 32, each unit in at
+                               most two K ranges, so ksplit is 2) instead of a K-split
+                               into rounds of work groups: deep products of 256 x 256
+                               tiles for which the planner chose a K-split, with at least
+                               eight blocks of units and no last tile column of at most
+                               128 columns; 0 otherwise */
 } fp64emu_layout_t;
 
 int fp64emu_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int nprimes, int use_corr,

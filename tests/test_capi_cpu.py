@@ -136,6 +136,13 @@ def test_layout_choices_fuzz():
         if not L.deep and L.ksplit == 1 and P >= 2 and L.Kp // 64 <= 32 and 0 < tiles < 256:
             assert L.gemm_tile_cols == 128, case
         assert (L.gemm_tile_rows, L.gemm_tile_cols) in ((256, 256), (256, 128), (128, 128)), case
+        if L.gemm_split:
+            T = (L.Mp // 256) * (L.Np // 256)
+            assert (L.ksplit, L.gemm_run, L.deep, L.nchunk) == (2, 1, 0, 1), case
+            assert (L.gemm_tile_rows, L.gemm_tile_cols) == (256, 256), case
+            assert L.ncorr == (2 if corr else 0) and L.Kp // 64 >= 256, case
+            assert T % 32 == 0 or 32 % T == 0, case
+            assert -(-(P + L.ncorr) * batch * T // 32) >= 8, case
         assert capi.workspace_size_min(batch, M, N, K, P, corr) <= L.total, case
 
 
@@ -299,6 +306,26 @@ def test_minimum_workspace(shape):
         assert 0 < wmin < full
     else:
         assert wmin == full
+
+
+def test_split_streams_only_for_deep_products_of_few_tiles():
+    """Split streams replace a K-split the planner chose for products of at
+    least 256 k-steps whose tiles per member and slot divide or are divided
+    by 32, with at least eight blocks of 32 units, and no mixed last tile
+    column; their two K ranges per unit are a K-split of 2."""
+    for shape in [(1, 1024, 2048, 32768, 15, True), (1, 1024, 1024, 32768, 15, True),
+                  (1, 1024, 2048, 16384, 14, True), (4, 512, 1024, 16384, 14, True),
+                  (1, 1023, 2048, 32769, 13, False), (1, 300, 2000, 17000, 15, True)]:
+        L = capi.layout(*shape)
+        assert (L.gemm_split, L.ksplit, L.gemm_run) == (1, 2, 1), shape
+    for shape in [(1, 1023, 2049, 32769, 15, True),    # c5: mixed last tile column
+                  (1, 1024, 1024, 8192, 14, True),     # 128 k-steps
+                  (1, 1500, 1500, 30000, 15, True),    # 36 tiles per slot
+                  (1, 3000, 1000, 20000, 14, True),    # 48 tiles per slot
+                  (1, 8192, 8192, 8192, 14, True),     # c2: no K-split
+                  (1, 512, 512, 65536, 15, True),      # 68 units: 3 blocks
+                  (1, 64, 40, 100_000, 15, True)]:     # narrow tiles
+        assert capi.layout(*shape).gemm_split == 0, shape
 
 
 def test_slot_runs_only_for_shallow_products():

@@ -596,3 +596,93 @@ def test_item_stream_random_whole_parity(dev):
         whole_parity(kind, A, B, O.PRIMES[:P], exact=exact, use_corr=corr)
         done += 1
         del A, B
+
+
+def _split_stream(L):
+    """The GEMM runs split streams: one work group per CU, each XCD's groups
+    over an eighth of the K-deep (tile, slot) units' k-steps in blocks of 32
+    units, with two K-split planes."""
+    return L.gemm_split == 1 and L.ksplit == 2 and not L.deep
+
+
+SPLIT_CASES = [
+    # kind, batch, M, N, K, moduli, corr -- units (tiles x slots) in the comment.
+    ("mm_nt", 1, 1000, 1000, 16384, O.PRIMES[:14], True),     # 256: 8 blocks, the fewest
+    ("mm", 1, 300, 2000, 17000, O.PRIMES[:15], True),         # 272: a last block of 16 units
+    ("bmm_nt", 2, 300, 1000, 20000, MODULI_ORDERS[1], True),  # 256 over 2 members, modulus 254
+    ("mm_nt", 1, 1000, 2000, 16384, O.PRIMES[:13], False),    # 416, no correction slots
+    ("mm", 1, 1000, 1000, 16384, O.PRIMES[:20], True),        # 352, every modulus
+    ("bmm", 2, 300, 1000, 20000, O.PRIMES[:15], True),        # 272 of 313 k-steps
+]
+
+
+@pytest.mark.parametrize("kind,batch,M,N,K,primes,corr", SPLIT_CASES)
+def test_split_stream_parity(dev, kind, batch, M, N, K, primes, corr):
+    """Deep products of few tiles run split streams (each unit in one or two
+    K ranges, a unit taken whole also storing zeros as its second split; the
+    workspace is filled with a nonzero byte first): every stage against the
+    oracle."""
+    from fp64_emu import capi
+    P = len(primes)
+    print(f"case split stream {kind} b={batch} {M}x{N}x{K} P={P} corr={corr}", flush=True)
+    assert _split_stream(capi.layout(batch, M, N, K, P, corr))
+    seed = 5100 + batch + M + N + K + P
+    if kind in ("bmm", "bmm_nt"):
+        A = _randn((batch, M, K), seed, dev)
+        B = _randn((batch, K, N) if kind == "bmm_nt" else (batch, N, K), seed + 1, dev)
+    else:
+        A = _randn((M, K), seed, dev)
+        B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
+    check_call(kind, A, B, primes, use_corr=corr)
+
+
+@pytest.mark.parametrize("P,corr", [(15, True), (13, False)])
+def test_split_stream_deep_whole_parity(dev, P, corr):
+    """c5's depth with 2048 columns (mm_nt 1023 x 2048 x 32769: 4 x 8 tiles,
+    units of 513 k-steps, 17 or 13 blocks of 32): the whole output bit for bit
+    against the oracle, the default plan and the reduced one."""
+    from fp64_emu import capi
+    from parity_util import whole_parity
+    M, N, K = 1023, 2048, 32769
+    print(f"case split stream whole mm_nt {M}x{N}x{K} P={P} corr={corr}", flush=True)
+    assert _split_stream(capi.layout(1, M, N, K, P, corr))
+    whole_parity("mm_nt", _randn((M, K), 6101, dev), _randn((K, N), 6102, dev), O.PRIMES[:P],
+                 use_corr=corr)
+
+
+def test_split_stream_random_whole_parity(dev):
+    """Six seeded random products that take split streams (mm and mm_nt, 12
+    to 20 moduli, with and without the correction, exact and fp64 combines;
+    normal, wide-range and integer entries): every output element bit for
+    bit against the oracle pipeline."""
+    from fp64_emu import capi
+    from parity_util import whole_parity
+    rng = np.random.default_rng(5301)
+    done = 0
+    while done < 6:
+        kind = str(rng.choice(["mm", "mm_nt"]))
+        M, N = int(rng.integers(250, 1100)), int(rng.integers(500, 2100))
+        K = int(rng.integers(16400, 33000))
+        P = int(rng.integers(12, 21))
+        corr, exact = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+        dist = int(rng.integers(0, 3))
+        seed = int(rng.integers(1 << 30))
+        if not _split_stream(capi.layout(1, M, N, K, P, corr)):
+            continue
+        print(f"case random split stream {kind} {M}x{N}x{K} P={P} corr={corr} exact={exact} "
+              f"dist={dist}", flush=True)
+        g = torch.Generator().manual_seed(seed)
+
+        def gen(shape):
+            if dist == 0:
+                return torch.randn(shape, dtype=torch.float64, generator=g)
+            if dist == 1:
+                s = torch.randint(0, 2, shape, generator=g) * 2 - 1
+                m = 1 + torch.rand(shape, generator=g, dtype=torch.float64)
+                return s * torch.ldexp(m, torch.randint(-30, 31, shape, generator=g))
+            return torch.randint(-2 ** 20, 2 ** 20 + 1, shape, generator=g).double()
+        A = gen((M, K)).to(dev)
+        B = gen((K, N) if kind == "mm_nt" else (N, K)).to(dev)
+        whole_parity(kind, A, B, O.PRIMES[:P], exact=exact, use_corr=corr)
+        done += 1
+        del A, B
