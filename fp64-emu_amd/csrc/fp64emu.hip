@@ -273,6 +273,9 @@ constexpr int kCUs = 256;
 // power limit and the time between items is no longer what bounds it.
 constexpr int kStreamChain = 8;
 constexpr int64_t kStreamMaxSteps = 64;
+// Split streams: a last tile column of at most kXMax columns is computed
+// beside the wide tiles (modgemm_tile's kXc).
+constexpr int kXMax = 2;
 constexpr int kMaxSplit = 16;
 
 int choose_ksplit(int64_t batch, int64_t tiles, int64_t nkt, int P, int ncorr, int64_t out_elems,
@@ -345,8 +348,8 @@ constexpr int64_t kRunMaxSteps = 32;
 // Mixed tiles: 256-column tiles whose last tile column holds at most 128
 // columns of N run that column as 128-column tiles in the same launch.
 bool use_mixed_tiles(const fp64emu_layout_t& L) {
-  return !L.deep && L.gemm_tile_cols == 256 && L.Np / kTileR >= 2 && L.N % kTileR != 0 &&
-         L.N % kTileR <= 128;
+  return !L.deep && !L.gemm_split && L.gemm_tile_cols == 256 && L.Np / kTileR >= 2 &&
+         L.N % kTileR != 0 && L.N % kTileR <= 128;
 }
 
 // Only 256 x 256 tiles run slots: the 256 x 128 and 128 x 128 launches hold
@@ -401,11 +404,17 @@ int slot_run_length(const fp64emu_layout_t& L) {
 // 3000 x 1000 x 20000 1.364 -> 1.374).  Not with a last tile column of at
 // most 128 columns (the mixed launch's half-width tiles).
 constexpr int64_t kSplitMinSteps = 256;
+// Extra columns: N mod 256 in 1 .. kXMax past at least one wide tile column.
+int split_extra_cols(const fp64emu_layout_t& L) {
+  const int r = (int)(L.N % kTileR);
+  return (L.Np / kTileR >= 2 && r >= 1 && r <= kXMax) ? r : 0;
+}
 bool use_split_streams(const fp64emu_layout_t& L) {
   if (L.deep || L.nchunk != 1 || L.ksplit < 2 || use_narrow_gemm(L)) return false;
-  if (L.Np / kTileR >= 2 && L.N % kTileR != 0 && L.N % kTileR <= 128) return false;
+  const int xc = split_extra_cols(L);
+  if (!xc && L.Np / kTileR >= 2 && L.N % kTileR != 0 && L.N % kTileR <= 128) return false;
   if (L.Kp / kTileK < kSplitMinSteps) return false;
-  const int64_t tiles = (L.Mp / kTileR) * (L.Np / kTileR);
+  const int64_t tiles = (L.Mp / kTileR) * (L.Np / kTileR - (xc ? 1 : 0));
   if (tiles % 32 != 0 && 32 % tiles != 0) return false;
   const int64_t units = (int64_t)(L.nprimes + (L.use_corr ? 2 : 0)) * L.batch * tiles;
   return (units + 31) / 32 >= 8;
@@ -498,7 +507,8 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   // first half of a 256-row plane tile past the last one holding data, so
   // the extraction skips the all-padding half there.
   L->ext_rowsA = L->gemm_tile_rows == 128 ? round_up(std::max<int64_t>(M, 1), 128) : L->chunk_rows;
-  L->ext_rowsB = (L->gemm_tile_cols == 128 || use_mixed_tiles(*L))
+  L->ext_rowsB = (L->gemm_tile_cols == 128 || use_mixed_tiles(*L) ||
+                  (L->gemm_split && split_extra_cols(*L) > 0))
                      ? round_up(std::max<int64_t>(N, 1), 128) : L->Np;
 }
 
@@ -1287,6 +1297,7 @@ struct GemmArgs {
   int run;             // residue slots per run group (1: one slot per group)
   int corr_run;        // 1: each tile's run starts with the (fused) correction slot
   int chain;           // item streams: items per work group
+  int xcols;           // split streams: extra columns past the TN wide tile columns
   int p[kMaxP];
   double invp[kMaxP];
 };
@@ -1350,6 +1361,15 @@ __device__ __forceinline__ void mma16(v4i& acc, const v4i& a, const v4i& b) {
 // other instruction ever writes an accumulator an MFMA then reads.
 __device__ __forceinline__ void mma16_init(v4i& acc, const v4i& a, const v4i& b) {
   asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, 0" : "=a"(acc) : "v"(a), "v"(b));
+}
+
+// acc += the dot product of the four int8 lanes of a and b, as inline
+// assembly: as a plain builtin the compiler sank a step's dot products past
+// the next barrier (pure arithmetic moves across the fences), bunching them
+// ahead of that step's first MFMA; in assembly they keep their place among
+// the MFMAs.
+__device__ __forceinline__ void dot4_acc(int& acc, int a, int b) {
+  asm volatile("v_dot4c_i32_i8 %0, %1, %2" : "+v"(acc) : "v"(a), "v"(b));
 }
 
 // 32 wait states, fenced against scheduling: more than any MFMA needs between
@@ -1503,9 +1523,10 @@ __device__ __forceinline__ void store_residue_block(const v4i (&acc)[kWM][kWN], 
 
 // One output tile of one slot (kRun: of it.nrun consecutive residue slots):
 // the body of the GEMM kernels, on the group's LDS ring `lds` (the kernel's
-// single LDS object).  kStream: an item stream; with kSplitS, a split stream.
+// single LDS object).  kStream: an item stream; with kSplitS, a split stream,
+// with kXc > 0 computing the kXc extra columns beside the last wide tiles.
 template <bool kDeep, int kWM, int kWN, bool kRun = false, bool kStream = false,
-          bool kSplitS = false>
+          bool kSplitS = false, int kXc = 0>
 __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, const GemmItem it) {
   using Sh = GemmShape<kWM, kWN>;
   constexpr int kSB = Sh::kSB, kDma = Sh::kDma, kHB = Sh::kHB;
@@ -1556,7 +1577,55 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   // tiles, to the next).
   const int8_t* cpA = At;
   const int8_t* cpB = Bt;
+  // Extra columns (kXc > 0, split streams): a product whose last tile column
+  // holds at most kXMax columns computes them beside its wide tiles, as VALU
+  // dot products over the A fragments a wide tile holds anyway: for each
+  // (slot, member, row tile), the unit in tile column (slot-member index mod
+  // TN) carries them, so that the carriers rotate over the tile columns and
+  // the XCD's groups.  Per stage, the 1 KiB B fragment of the extra columns
+  // (16 plane rows, the first of the last tile) lands after the ring (each
+  // wave copying a quarter); cpX is its copy source for the stage being
+  // copied (null: that stage's unit carries none), xon marks a carrier's
+  // piece, XR holds the current k-step's 16 bytes of each column for the
+  // lane's k group, xacc the partial sums of the wave's rows (the wn = 0
+  // wave its first four 16-row fragments, the wn = 1 wave its last four),
+  // summed over the lanes' four k groups at the piece's end.
+  // kXon: 1 + the first of the four fragments the k-steps being compiled take
+  // (0: none) -- blocks of the split branch redeclare it, so that their steps
+  // carry the dot products unconditionally and other steps none.  (The dot
+  // products of a k-step sit after its last MFMAs, while those drain: placed
+  // between the MFMAs they delayed them, and the whole call, more.)
+  const int8_t* cpX = nullptr;
+  bool xon = false;
+  constexpr int kXon = 0;
+  v4i XR[kXc > 0 ? kXc : 1];
+  int xacc[kWM][kXc > 0 ? kXc : 1];
+  constexpr int kXBase = Sh::kLdsBytes;
 #define FP64EMU_SLOT(kt) ((kS == 4) ? ((kt) & 3) : ((kt) % kS))
+#define FP64EMU_COPY_X(kt)                                                                  \
+  do {                                                                                      \
+    if constexpr (kXc > 0) {                                                                \
+      if (cpX != nullptr && lane < 16)                                                      \
+        copy_lds16<0>(cpX + wave * 256 + lane * 16,                                         \
+                      (lds_i8*)(lds + kXBase + FP64EMU_SLOT(kt) * 1024 + wave * 256));      \
+    }                                                                                       \
+  } while (0)
+#define FP64EMU_READX(kt)                                                                   \
+  do {                                                                                      \
+    if constexpr (kXc > 0) {                                                                \
+      _Pragma("unroll") for (int ci_ = 0; ci_ < kXc; ++ci_)                                 \
+        XR[ci_] = *reinterpret_cast<const v4i*>(lds + kXBase + FP64EMU_SLOT(kt) * 1024 +     \
+                                                (lane >> 4) * 256 + ci_ * 16);              \
+    }                                                                                       \
+  } while (0)
+  // The extra columns' dot products of A fragment x_ at dword d_.
+#define FP64EMU_XDOT(FC, x_, d_)                                                             \
+  do {                                                                                      \
+    if constexpr (kXc > 0) {                                                                \
+      _Pragma("unroll") for (int ci_ = 0; ci_ < kXc; ++ci_)                                 \
+        dot4_acc(xacc[x_][ci_], FC[x_][d_], XR[ci_][d_]);                                   \
+    }                                                                                       \
+  } while (0)
 #define FP64EMU_COPY_A(kt, j)                                                               \
   copy_lds16<(j) * 1024>((kRun || kStream ? cpA : At + (int64_t)(kt) * kTileBytes) + goff,   \
                          (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + wave * (kWM / 2) * 1024))
@@ -1565,6 +1634,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
                          (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + kAB + wave * (kWN / 2) * 1024))
 #define FP64EMU_ISSUE(kt)                                                              \
   do {                                                                                 \
+    FP64EMU_COPY_X(kt);                                                                \
     FP64EMU_COPY_A(kt, 0);                                                             \
     FP64EMU_COPY_A(kt, 1);                                                             \
     if constexpr (kWM == 8) {                                                          \
@@ -1607,6 +1677,12 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     if ((kt) + kPF < nk) FP64EMU_ISSUE((kt) + kPF);                                      \
     FP64EMU_READF(FN, (kt) + 1);                                                         \
     FP64EMU_MMA(FC, MMA);                                                                \
+    if constexpr (kXc > 0 && kXon > 0) {                                                 \
+      _Pragma("unroll") for (int d_ = 0; d_ < 4; ++d_)                                   \
+      _Pragma("unroll") for (int x_ = 0; x_ < 4; ++x_)                                   \
+        FP64EMU_XDOT(FC, kXon - 1 + x_, d_);                                             \
+      FP64EMU_READX((kt) + 1);                                                           \
+    }                                                                                    \
   } while (0)
   // Steady-state step (a copy for step kt+3 exists): an unconditional wait,
   // so the compiler's own wait tracking sees every earlier fragment read
@@ -1636,6 +1712,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     const v4i* sa_ = reinterpret_cast<const v4i*>(lds + FP64EMU_SLOT((kt) + 1) * kSB);      \
     const v4i* sb_ = sa_ + kTileBytes / 16;                                                  \
     _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                          \
+      if (j == 0 && (c) == 0) FP64EMU_COPY_X((kt) + kPF);                                      \
       if (j == 0 && ((c) >> 1) == 0) FP64EMU_COPY_A((kt) + kPF, ((c) & 1) * 2);                \
       if (j == 2 && ((c) >> 1) == 0) FP64EMU_COPY_A((kt) + kPF, ((c) & 1) * 2 + 1);            \
       if (j == 0 && ((c) >> 1) == 1) FP64EMU_COPY_B((kt) + kPF, ((c) & 1) * 2);                \
@@ -1648,6 +1725,14 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
       _Pragma("unroll") for (int u = 0; u < 4; ++u) {                                        \
         const int m_ = 4 * j + u, x = (c) * 2 + m_ / 8, y = (m_ < 8) ? m_ : 15 - m_;           \
         MMA(acc[x][y], FC[x], FC[8 + y]);                                                    \
+      }                                                                                      \
+      if constexpr (kXc > 0 && kXon > 0) {                                                   \
+        if ((c) == 3 && j == 3) {                                                            \
+          _Pragma("unroll") for (int d_ = 0; d_ < 4; ++d_)                                   \
+          _Pragma("unroll") for (int x_ = 0; x_ < 4; ++x_)                                   \
+            FP64EMU_XDOT(FC, kXon - 1 + x_, d_);                                             \
+          FP64EMU_READX((kt) + 1);                                                           \
+        }                                                                                    \
       }                                                                                      \
       __builtin_amdgcn_sched_barrier(0);                                                     \
     }                                                                                        \
@@ -1749,6 +1834,11 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   do {                                                                                      \
     v4i F0[kWM + kWN], F1[kWM + kWN];                                                       \
     FP64EMU_READF(F0, (G0));                                                                \
+    if constexpr (kXc > 0 && kXon > 0) {                                                    \
+      FP64EMU_READX((G0));                                                                  \
+      _Pragma("unroll") for (int x_ = 0; x_ < kWM; ++x_)                                    \
+      _Pragma("unroll") for (int ci_ = 0; ci_ < kXc; ++ci_) xacc[x_][ci_] = 0;              \
+    }                                                                                       \
     FP64EMU_RSTEP_R((G0), F0, F1, mma16_init);                                              \
     int kt_ = 1;                                                                            \
     const int kf_ = nk - kPF - (G0);   /* steps kt_ < kf_ copy stage G0 + kt_ + kPF */      \
@@ -1865,6 +1955,10 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     // 1; a piece covering its unit whole also stores zeros as split 1.
     const int x = (int)(blockIdx.x & 7u);
     const uint32_t jl = blockIdx.x >> 3;
+    // Extra columns: the unit in tile column nt of slot-member sb carries them.
+    auto x_carrier = [&](const int nt_, const uint32_t sb_) {
+      return nt_ == (int)(sb_ % (uint32_t)g.TN);
+    };
     const uint32_t U = (uint32_t)g.total;
     const uint32_t nblk = (U + 31u) >> 5;
     const int64_t Tb = (int64_t)nblk * g.nkt;
@@ -1882,6 +1976,8 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     int cleft = 0;
     const int8_t* nA = nullptr;
     const int8_t* nB = nullptr;
+    const int8_t* nX = nullptr;   // kXc: the extra columns' fragment (B's tile g.TN)
+    bool nXon = false;
     int64_t cend = e0 - (int64_t)cbl * g.nkt;               // stream end, from the piece's block
     auto copy_piece = [&](const int k) {
       const GemmItem t = stream_item(g, cbl * 32u + jl);
@@ -1891,6 +1987,10 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
       const int k0 = (ic ? t.slot * g.nkt : 0) + k;
       nA = g.A + t.b * g.memberA + (int64_t)pl * g.planeA + ((int64_t)t.mt * rs + k0) * kTileBytes;
       nB = g.B + t.b * g.memberB + (int64_t)pl * g.planeB + ((int64_t)t.nt * rs + k0) * kTileBytes;
+      if constexpr (kXc > 0) {
+        nXon = x_carrier(t.nt, (cbl * 32u + jl) / (uint32_t)(g.TM * g.TN));
+        nX = g.B + t.b * g.memberB + (int64_t)pl * g.planeB + ((int64_t)g.TN * rs + k0) * kTileBytes;
+      }
       cleft = (int)min<int64_t>(g.nkt, cend) - k;
     };
     copy_piece(kfirst);
@@ -1899,6 +1999,10 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
       cpB = nB;
       nA += kTileBytes;
       nB += kTileBytes;
+      if constexpr (kXc > 0) {
+        cpX = nXon ? nX : nullptr;
+        nX += kTileBytes;
+      }
       if (__builtin_expect(--cleft == 0, 0) && cend > g.nkt) {
         ++cbl;
         cend -= g.nkt;
@@ -1916,11 +2020,40 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     int k0 = kfirst;
     while (G0 < nk) {
       const int nj = min(g.nkt - k0, nk - G0);
-      FP64EMU_STREAM_SLOT(G0, nj);
       const GemmItem t = stream_item(g, bl * 32u + jl);
+      // A carrier of the extra columns: this wave's fragments 4 wn .. 4 wn + 3.
+      xon = kXc > 0 && x_carrier(t.nt, (bl * 32u + jl) / (uint32_t)(g.TM * g.TN));
+      if (kXc > 0 && xon && wn == 0) {
+        constexpr int kXon = 1;
+        FP64EMU_STREAM_SLOT(G0, nj);
+      } else if (kXc > 0 && xon) {
+        constexpr int kXon = 5;
+        FP64EMU_STREAM_SLOT(G0, nj);
+      } else {
+        FP64EMU_STREAM_SLOT(G0, nj);
+      }
       const bool whole = k0 == 0 && nj == g.nkt;
       const int64_t sbm = (int64_t)(k0 == 0 ? 0 : 1) * g.batch + t.b;   // split-major planes
       const int64_t rb0 = (int64_t)t.mt * (2 * kWM) + wm * kWM, cb0 = (int64_t)t.nt * (kWN / 2) + wn * kHB;
+      // Extra columns: sums over the four k groups (lanes l, l ^ 16, l ^ 32,
+      // l ^ 48 hold row l % 16's); lane r < 16 then stores row r of each
+      // fragment, element 256 (r / 4) + 16 ci + r % 4 of the 16 x 64 output
+      // block (column ci) in column block 4 g.TN.
+      const int64_t cbX = (int64_t)g.TN * 4;
+      const int xel = 256 * (lane >> 2) + (lane & 3);
+      auto xsum = [&]() {
+        if constexpr (kXc > 0) {
+#pragma unroll
+          for (int x_ = 0; x_ < kWM; ++x_)
+#pragma unroll
+            for (int ci_ = 0; ci_ < kXc; ++ci_) {
+              int v = xacc[x_][ci_];
+              v += __shfl_xor(v, 16);
+              v += __shfl_xor(v, 32);
+              xacc[x_][ci_] = v;
+            }
+        }
+      };
       if (t.slot < g.ncorr) {
         int32_t* cdst = g.corr + (sbm * g.ncorr + t.slot) * g.outplane;
         const int64_t zoff = (int64_t)g.batch * g.ncorr * g.outplane;   // split 1, in int32s
@@ -1941,6 +2074,22 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
             }
             __builtin_amdgcn_sched_barrier(0);
           }
+        if constexpr (kXc > 0) {
+          if (xon) {
+            xsum();
+            if (lane < 16) {
+#pragma unroll
+              for (int x_ = 0; x_ < kWM; ++x_)
+#pragma unroll
+                for (int ci_ = 0; ci_ < kXc; ++ci_) {
+                  if ((x_ >> 2) != wn) continue;   // the other wave's fragment
+                  int32_t* c = cdst + ((rb0 + x_) * NB + cbX) * 1024 + xel + 16 * ci_;
+                  *c = xacc[x_][ci_];
+                  if (whole) c[zoff] = 0;
+                }
+            }
+          }
+        }
       } else {
         const int tp = t.slot - g.ncorr;
         const double ip = g.invp[tp];
@@ -1956,6 +2105,24 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
             if (whole) *reinterpret_cast<v4i*>(d + zoff) = v4i{0, 0, 0, 0};
             __builtin_amdgcn_sched_barrier(0);
           }
+        if constexpr (kXc > 0) {
+          if (xon) {
+            xsum();
+            if (lane < 16) {
+#pragma unroll
+              for (int x_ = 0; x_ < kWM; ++x_)
+#pragma unroll
+                for (int ci_ = 0; ci_ < kXc; ++ci_) {
+                  if ((x_ >> 2) != wn) continue;   // the other wave's fragment
+                  const int v = xacc[x_][ci_];
+                  const int q = __double2loint(fma((double)v, ip, kMagic));
+                  int8_t* d = rdst + ((rb0 + x_) * NB + cbX) * 1024 + xel + 16 * ci_;
+                  *d = (int8_t)(__mul24(q, negp) + v);   // the balanced residue's byte
+                  if (whole) d[zoff] = 0;
+                }
+            }
+          }
+        }
       }
       G0 += nj;
       ++bl;
@@ -2100,6 +2267,9 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
 #undef FP64EMU_STREAM_SLOT
 #undef FP64EMU_COPY_A
 #undef FP64EMU_COPY_B
+#undef FP64EMU_COPY_X
+#undef FP64EMU_READX
+#undef FP64EMU_XDOT
 #undef FP64EMU_SLOT
 
   // Epilogue (of a single slot; a run stores each slot as it ends).
@@ -2245,6 +2415,17 @@ __global__ void __launch_bounds__(kThreads, 1)
 modgemm_split_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) int8_t lds[GemmShape<8, 8>::kLdsBytes];
   modgemm_tile<false, 8, 8, false, true, true>(g, lds, GemmItem{});
+}
+
+// Split streams with kXc = g.xcols extra columns (a last tile column of at
+// most kXMax columns): the ring plus 1 KiB per stage for their B fragment.
+template <int kXc>
+__global__ void __launch_bounds__(kThreads, 1)
+modgemm_split_x_kernel(GemmArgs g) {
+  constexpr int kBytes = GemmShape<8, 8>::kLdsBytes + GemmShape<8, 8>::kS * 1024;
+  static_assert(kBytes <= 160 * 1024, "LDS ring and extra-column stages exceed the CU's 160 KiB");
+  __shared__ __attribute__((aligned(1024))) int8_t lds[kBytes];
+  modgemm_tile<false, 8, 8, false, true, true, kXc>(g, lds, GemmItem{});
 }
 
 // ---------------------------------------------------------------------------
@@ -3211,7 +3392,10 @@ int run(const Call& c) {
   const int64_t vslots = ga.corr_run ? 1 : L.ncorr + (c.P + ga.run - 1) / ga.run;
   ga.total = vslots * c.batch * L.ksplit * ga.TM * ga.TN;
   // Split streams: g.total counts the K-deep units (the correction products
-  // as two slots: ncorr is 2), which 256 groups share.
+  // as two slots: ncorr is 2), which 256 groups share; extra columns (a last
+  // tile column of at most kXMax columns) ride on the last wide tile column.
+  ga.xcols = L.gemm_split ? split_extra_cols(L) : 0;
+  if (ga.xcols) ga.TN -= 1;
   if (L.gemm_split) ga.total = (int64_t)ga.nslots * c.batch * ga.TM * ga.TN;
   // 256 x 256 tiles one slot per item of at most kStreamMaxSteps k-steps, no
   // K-split, at least two items per CU: groups of kStreamChain items, each
@@ -3336,7 +3520,11 @@ int run(const Call& c) {
       ga.first = seg == 0 ? 1 : 0;
       if (L.deep)
         hipLaunchKernelGGL((modgemm_kernel<true, 8, 8>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);
-      else if (L.gemm_split)   // 256 x 256 tiles, K-split 2 (use_split_streams)
+      else if (L.gemm_split && ga.xcols == 1)   // 256 x 256 tiles, K-split 2 (use_split_streams)
+        hipLaunchKernelGGL(modgemm_split_x_kernel<1>, dim3(kCUs), dim3(kThreads), 0, s, ga);
+      else if (L.gemm_split && ga.xcols == 2)
+        hipLaunchKernelGGL(modgemm_split_x_kernel<2>, dim3(kCUs), dim3(kThreads), 0, s, ga);
+      else if (L.gemm_split)
         hipLaunchKernelGGL(modgemm_split_kernel, dim3(kCUs), dim3(kThreads), 0, s, ga);
       else if (ga.run > 1)   // 256 x 256 tiles only (use_slot_runs)
         hipLaunchKernelGGL((modgemm_kernel<false, 8, 8, true>), dim3((unsigned)ga.total), dim3(kThreads), 0, s, ga);

@@ -137,7 +137,8 @@ def test_layout_choices_fuzz():
             assert L.gemm_tile_cols == 128, case
         assert (L.gemm_tile_rows, L.gemm_tile_cols) in ((256, 256), (256, 128), (128, 128)), case
         if L.gemm_split:
-            T = (L.Mp // 256) * (L.Np // 256)
+            xc = N % 256 if (L.Np // 256 >= 2 and 1 <= N % 256 <= 2) else 0
+            T = (L.Mp // 256) * (L.Np // 256 - (1 if xc else 0))
             assert (L.ksplit, L.gemm_run, L.deep, L.nchunk) == (2, 1, 0, 1), case
             assert (L.gemm_tile_rows, L.gemm_tile_cols) == (256, 256), case
             assert L.ncorr == (2 if corr else 0) and L.Kp // 64 >= 256, case
@@ -310,15 +311,20 @@ def test_minimum_workspace(shape):
 
 def test_split_streams_only_for_deep_products_of_few_tiles():
     """Split streams replace a K-split the planner chose for products of at
-    least 256 k-steps whose tiles per member and slot divide or are divided
-    by 32, with at least eight blocks of 32 units, and no mixed last tile
-    column; their two K ranges per unit are a K-split of 2."""
+    least 256 k-steps whose wide tiles per member and slot divide or are
+    divided by 32, with at least eight blocks of 32 units; a last tile column
+    of one or two columns rides on the wide tiles (c5), one of 3 to 128
+    columns keeps the mixed launch.  Their two K ranges per unit are a
+    K-split of 2."""
     for shape in [(1, 1024, 2048, 32768, 15, True), (1, 1024, 1024, 32768, 15, True),
                   (1, 1024, 2048, 16384, 14, True), (4, 512, 1024, 16384, 14, True),
-                  (1, 1023, 2048, 32769, 13, False), (1, 300, 2000, 17000, 15, True)]:
+                  (1, 1023, 2048, 32769, 13, False), (1, 300, 2000, 17000, 15, True),
+                  (1, 1023, 2049, 32769, 15, True), (1, 1023, 2049, 32769, 13, False),
+                  (1, 500, 2050, 17000, 15, True), (2, 512, 1025, 20000, 14, True)]:
         L = capi.layout(*shape)
         assert (L.gemm_split, L.ksplit, L.gemm_run) == (1, 2, 1), shape
-    for shape in [(1, 1023, 2049, 32769, 15, True),    # c5: mixed last tile column
+    assert capi.layout(1, 1023, 2049, 32769, 15, True).ext_rowsB == 2176   # B rows to 128 past N
+    for shape in [(1, 1023, 2051, 32769, 15, True),    # three columns past: mixed tiles
                   (1, 1024, 1024, 8192, 14, True),     # 128 k-steps
                   (1, 1500, 1500, 30000, 15, True),    # 36 tiles per slot
                   (1, 3000, 1000, 20000, 14, True),    # 48 tiles per slot

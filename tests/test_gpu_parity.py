@@ -686,3 +686,76 @@ def test_split_stream_random_whole_parity(dev):
         whole_parity(kind, A, B, O.PRIMES[:P], exact=exact, use_corr=corr)
         done += 1
         del A, B
+
+
+SPLIT_X_CASES = [
+    # kind, batch, M, N, K, moduli, corr -- extra columns past the wide tiles in the comment.
+    ("mm_nt", 1, 1000, 1025, 16384, O.PRIMES[:14], True),     # 1 past 4 tile columns
+    ("mm", 1, 500, 2050, 17000, O.PRIMES[:15], True),         # 2 past 8
+    ("bmm_nt", 2, 512, 1025, 20000, MODULI_ORDERS[1], True),  # 1, two members, modulus 254
+    ("mm_nt", 1, 1000, 2049, 16384, O.PRIMES[:13], False),    # 1 past 8, no correction slots
+    ("mm", 1, 1000, 1026, 16384, O.PRIMES[:20], True),        # 2, every modulus
+]
+
+
+@pytest.mark.parametrize("kind,batch,M,N,K,primes,corr", SPLIT_X_CASES)
+def test_split_stream_extra_column_parity(dev, kind, batch, M, N, K, primes, corr):
+    """A last tile column of one or two columns of N under split streams:
+    the units of the last wide tile column compute those columns beside
+    their tiles (VALU dot products over the same A fragments, the columns'
+    B fragment copied with each stage): every stage against the oracle, on a
+    workspace filled with a nonzero byte first."""
+    from fp64_emu import capi
+    P = len(primes)
+    print(f"case split stream extra columns {kind} b={batch} {M}x{N}x{K} P={P} corr={corr}",
+          flush=True)
+    L = capi.layout(batch, M, N, K, P, corr)
+    assert _split_stream(L) and 1 <= N % 256 <= 2
+    seed = 5700 + batch + M + N + K + P
+    if kind in ("bmm", "bmm_nt"):
+        A = _randn((batch, M, K), seed, dev)
+        B = _randn((batch, K, N) if kind == "bmm_nt" else (batch, N, K), seed + 1, dev)
+    else:
+        A = _randn((M, K), seed, dev)
+        B = _randn((K, N) if kind == "mm_nt" else (N, K), seed + 1, dev)
+    check_call(kind, A, B, primes, use_corr=corr)
+
+
+def test_split_stream_extra_column_random_whole_parity(dev):
+    """Six seeded random products with one or two columns past their wide
+    tiles under split streams (mm and mm_nt, 12 to 20 moduli, with and
+    without the correction, exact and fp64 combines; normal, wide-range and
+    integer entries): every output element bit for bit against the oracle
+    pipeline."""
+    from fp64_emu import capi
+    from parity_util import whole_parity
+    rng = np.random.default_rng(5417)
+    done = 0
+    while done < 6:
+        kind = str(rng.choice(["mm", "mm_nt"]))
+        M = int(rng.integers(250, 1100))
+        N = 256 * int(rng.integers(2, 9)) + int(rng.integers(1, 3))
+        K = int(rng.integers(16400, 33000))
+        P = int(rng.integers(12, 21))
+        corr, exact = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+        dist = int(rng.integers(0, 3))
+        seed = int(rng.integers(1 << 30))
+        if not _split_stream(capi.layout(1, M, N, K, P, corr)):
+            continue
+        print(f"case random split stream extra columns {kind} {M}x{N}x{K} P={P} corr={corr} "
+              f"exact={exact} dist={dist}", flush=True)
+        g = torch.Generator().manual_seed(seed)
+
+        def gen(shape):
+            if dist == 0:
+                return torch.randn(shape, dtype=torch.float64, generator=g)
+            if dist == 1:
+                s = torch.randint(0, 2, shape, generator=g) * 2 - 1
+                m = 1 + torch.rand(shape, generator=g, dtype=torch.float64)
+                return s * torch.ldexp(m, torch.randint(-30, 31, shape, generator=g))
+            return torch.randint(-2 ** 20, 2 ** 20 + 1, shape, generator=g).double()
+        A = gen((M, K)).to(dev)
+        B = gen((K, N) if kind == "mm_nt" else (N, K)).to(dev)
+        whole_parity(kind, A, B, O.PRIMES[:P], exact=exact, use_corr=corr)
+        done += 1
+        del A, B
