@@ -505,11 +505,14 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
   L->gemm_run = use_slot_runs(*L) ? slot_run_length(*L) : 1;
   // Plane rows the GEMM reads: 128-row (128-column) tiles read only the
   // first half of a 256-row plane tile past the last one holding data, so
-  // the extraction skips the all-padding half there.
+  // the extraction skips the all-padding half there; a split stream's extra
+  // columns read only the last tile's first 16 rows (a 64-row group).
   L->ext_rowsA = L->gemm_tile_rows == 128 ? round_up(std::max<int64_t>(M, 1), 128) : L->chunk_rows;
-  L->ext_rowsB = (L->gemm_tile_cols == 128 || use_mixed_tiles(*L) ||
-                  (L->gemm_split && split_extra_cols(*L) > 0))
-                     ? round_up(std::max<int64_t>(N, 1), 128) : L->Np;
+  if (L->gemm_split && split_extra_cols(*L) > 0)
+    L->ext_rowsB = round_up(N, 64);
+  else
+    L->ext_rowsB = (L->gemm_tile_cols == 128 || use_mixed_tiles(*L))
+                       ? round_up(std::max<int64_t>(N, 1), 128) : L->Np;
 }
 
 // ---------------------------------------------------------------------------

@@ -208,7 +208,7 @@ typedef struct {
                                leaves runs of one) */
   int64_t ext_rowsA;        /* rows of each A plane (per member, per row chunk) that the
                                extraction writes: the operand rows and the zero padding
-                               that GEMM tiles read (a multiple of 128, at most the padded
+                               that GEMM tiles read (a multiple of 64, at most the padded
                                row count); rows past it hold unspecified bytes */
   int64_t ext_rowsB;        /* the same for B's plane rows (the columns of B^T) */
   int gemm_split;           /* 1: the modular GEMM runs as split streams (one work group

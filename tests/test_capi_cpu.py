@@ -88,11 +88,14 @@ def test_layout_consistency(shape, P, corr):
     assert L.outplane_bytes == L.Mp * L.Np
     # Extracted plane rows: every operand row, a multiple of 128, within the
     # padded plane; short of it only where GEMM tiles are 128 wide.
-    # (B also under mixed tiles, whose last tile column is read 128 wide.)
-    for ext, R, Rp, short_ok in ((L.ext_rowsA, M, L.chunk_rows, L.gemm_tile_rows == 128),
-                                 (L.ext_rowsB, N, L.Np, not deep)):
-        assert ext % 128 == 0 and min(max(R, 1), Rp) <= ext <= Rp
-        assert ext == Rp or (short_ok and ext == -(-max(R, 1) // 128) * 128)
+    # (B also under mixed tiles, whose last tile column is read 128 wide,
+    # and to a multiple of 64 under split streams with extra columns, which
+    # read 16 rows of the last tile.)
+    xcols = L.gemm_split and L.Np // 256 >= 2 and 1 <= N % 256 <= 2
+    for ext, R, Rp, short_ok, q in ((L.ext_rowsA, M, L.chunk_rows, L.gemm_tile_rows == 128, 128),
+                                    (L.ext_rowsB, N, L.Np, not deep, 64 if xcols else 128)):
+        assert ext % q == 0 and min(max(R, 1), Rp) <= ext <= Rp
+        assert ext == Rp or (short_ok and ext == -(-max(R, 1) // q) * q)
     sizes = [("off_sftA", 2 * batch * M), ("off_sftB", 2 * batch * N), ("off_lgA", 4 * batch * M),
              ("off_lgB", 4 * batch * N), ("off_bits", 16), ("off_pmax", 8 * L.nslab * batch * N),
              ("off_pss", 8 * L.nslab * batch * N), ("off_planesA", batch * L.memberA_bytes),
@@ -323,7 +326,7 @@ def test_split_streams_only_for_deep_products_of_few_tiles():
                   (1, 500, 2050, 17000, 15, True), (2, 512, 1025, 20000, 14, True)]:
         L = capi.layout(*shape)
         assert (L.gemm_split, L.ksplit, L.gemm_run) == (1, 2, 1), shape
-    assert capi.layout(1, 1023, 2049, 32769, 15, True).ext_rowsB == 2176   # B rows to 128 past N
+    assert capi.layout(1, 1023, 2049, 32769, 15, True).ext_rowsB == 2112   # B rows to 64 past N
     for shape in [(1, 1023, 2051, 32769, 15, True),    # three columns past: mixed tiles
                   (1, 1024, 1024, 8192, 14, True),     # 128 k-steps
                   (1, 1500, 1500, 30000, 15, True),    # 36 tiles per slot
