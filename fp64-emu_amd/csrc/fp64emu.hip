@@ -266,7 +266,8 @@ constexpr int kCUs = 256;
 // than kRunMaxSteps and at most kStreamMaxSteps k-steps.  Measured against
 // one item per group, whole calls in one process: 4096^2 x 2560 0.784 ->
 // 0.766 ms, 4096^2 x 3072 0.900 -> 0.873, 3000^3 0.554 -> 0.537, 4096^3
-// 1.120 -> 1.100 at 8 items per group (2 and 4 gained less); even at
+// 1.120 -> 1.100 at 8 items per group (2 and 4 gained less, 16 the same as
+// 8: 4096^3 1.123 against 1.126 ms, one group per CU there); even at
 // 6144^2 x 3072, 6144^2 x 4096 and 8192^2 x 4096; slower from 80 k-steps
 // (5120^3 2.02 -> 2.05, 4096^2 x 8192 2.017 -> 2.04, 8192^3 7.14 -> 7.30 at
 // 2 items, 7.45 at one group per CU), where the GEMM runs at the part's
