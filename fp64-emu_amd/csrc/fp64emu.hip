@@ -1586,48 +1586,45 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
   // dot products over the A fragments a wide tile holds anyway: for each
   // (slot, member, row tile), the unit in tile column (slot-member index mod
   // TN) carries them, so that the carriers rotate over the tile columns and
-  // the XCD's groups.  Per stage, the 1 KiB B fragment of the extra columns
-  // (16 plane rows, the first of the last tile) lands after the ring (each
-  // wave copying a quarter); cpX is its copy source for the stage being
-  // copied (null: that stage's unit carries none), xon marks a carrier's
-  // piece, XR holds the current k-step's 16 bytes of each column for the
-  // lane's k group, xacc the partial sums of the wave's rows (the wn = 0
-  // wave its first four 16-row fragments, the wn = 1 wave its last four),
-  // summed over the lanes' four k groups at the piece's end.
+  // the XCD's groups.  A carrier's waves load the columns' bytes of each
+  // k-step straight from B's plane (the first 16 rows of its last tile, the
+  // 16 bytes of each column for the lane's k group) two steps ahead, into the
+  // buffer XR_F0 or XR_F1 that pairs with the step's fragment buffer (so the
+  // buffer of a step is the one its own load filled two steps before); xsrc
+  // is that fragment at the piece's first step xg0, xg_last the piece's last
+  // step (loads past it reread it).  xon marks a carrier's piece, xacc the
+  // partial sums of the wave's rows (the wn = 0 wave its first four 16-row
+  // fragments, the wn = 1 wave its last four), summed over the lanes' four k
+  // groups at the piece's end.
   // kXon: 1 + the first of the four fragments the k-steps being compiled take
   // (0: none) -- blocks of the split branch redeclare it, so that their steps
   // carry the dot products unconditionally and other steps none.  (The dot
   // products of a k-step sit after its last MFMAs, while those drain: placed
   // between the MFMAs they delayed them, and the whole call, more.)
-  const int8_t* cpX = nullptr;
   bool xon = false;
   constexpr int kXon = 0;
-  v4i XR[kXc > 0 ? kXc : 1];
+  const int8_t* xsrc = nullptr;
+  int xg0 = 0, xg_last = 0;
+  v4i XR_F0[kXc > 0 ? kXc : 1], XR_F1[kXc > 0 ? kXc : 1];
   int xacc[kWM][kXc > 0 ? kXc : 1];
-  constexpr int kXBase = Sh::kLdsBytes;
 #define FP64EMU_SLOT(kt) ((kS == 4) ? ((kt) & 3) : ((kt) % kS))
-#define FP64EMU_COPY_X(kt)                                                                  \
+  // The extra columns' bytes of stream step G into buffer XB.
+#define FP64EMU_XLOAD(XB, G)                                                                \
   do {                                                                                      \
-    if constexpr (kXc > 0) {                                                                \
-      if (cpX != nullptr && lane < 16)                                                      \
-        copy_lds16<0>(cpX + wave * 256 + lane * 16,                                         \
-                      (lds_i8*)(lds + kXBase + FP64EMU_SLOT(kt) * 1024 + wave * 256));      \
+    if constexpr (kXc > 0 && kXon > 0) {                                                    \
+      const int8_t* xp_ = xsrc + (int64_t)(min((G), xg_last) - xg0) * kTileBytes +          \
+                          (lane >> 4) * 256;                                                \
+      _Pragma("unroll") for (int ci_ = 0; ci_ < kXc; ++ci_)                                 \
+        XB[ci_] = *reinterpret_cast<const v4i*>(xp_ + ci_ * 16);                            \
     }                                                                                       \
   } while (0)
-#define FP64EMU_READX(kt)                                                                   \
+  // The extra columns' dot products of A fragment x_ at dword d_ (XB: the
+  // step's X buffer).
+#define FP64EMU_XDOT(FC, XB, x_, d_)                                                         \
   do {                                                                                      \
     if constexpr (kXc > 0) {                                                                \
       _Pragma("unroll") for (int ci_ = 0; ci_ < kXc; ++ci_)                                 \
-        XR[ci_] = *reinterpret_cast<const v4i*>(lds + kXBase + FP64EMU_SLOT(kt) * 1024 +     \
-                                                (lane >> 4) * 256 + ci_ * 16);              \
-    }                                                                                       \
-  } while (0)
-  // The extra columns' dot products of A fragment x_ at dword d_.
-#define FP64EMU_XDOT(FC, x_, d_)                                                             \
-  do {                                                                                      \
-    if constexpr (kXc > 0) {                                                                \
-      _Pragma("unroll") for (int ci_ = 0; ci_ < kXc; ++ci_)                                 \
-        dot4_acc(xacc[x_][ci_], FC[x_][d_], XR[ci_][d_]);                                   \
+        dot4_acc(xacc[x_][ci_], FC[x_][d_], XB[ci_][d_]);                                   \
     }                                                                                       \
   } while (0)
 #define FP64EMU_COPY_A(kt, j)                                                               \
@@ -1638,7 +1635,6 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
                          (lds_i8*)(lds + FP64EMU_SLOT(kt) * kSB + kAB + wave * (kWN / 2) * 1024))
 #define FP64EMU_ISSUE(kt)                                                              \
   do {                                                                                 \
-    FP64EMU_COPY_X(kt);                                                                \
     FP64EMU_COPY_A(kt, 0);                                                             \
     FP64EMU_COPY_A(kt, 1);                                                             \
     if constexpr (kWM == 8) {                                                          \
@@ -1684,8 +1680,8 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     if constexpr (kXc > 0 && kXon > 0) {                                                 \
       _Pragma("unroll") for (int d_ = 0; d_ < 4; ++d_)                                   \
       _Pragma("unroll") for (int x_ = 0; x_ < 4; ++x_)                                   \
-        FP64EMU_XDOT(FC, kXon - 1 + x_, d_);                                             \
-      FP64EMU_READX((kt) + 1);                                                           \
+        FP64EMU_XDOT(FC, XR_##FC, kXon - 1 + x_, d_);                                    \
+      FP64EMU_XLOAD(XR_##FC, (kt) + 2);                                                  \
     }                                                                                    \
   } while (0)
   // Steady-state step (a copy for step kt+3 exists): an unconditional wait,
@@ -1716,7 +1712,6 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     const v4i* sa_ = reinterpret_cast<const v4i*>(lds + FP64EMU_SLOT((kt) + 1) * kSB);      \
     const v4i* sb_ = sa_ + kTileBytes / 16;                                                  \
     _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                          \
-      if (j == 0 && (c) == 0) FP64EMU_COPY_X((kt) + kPF);                                      \
       if (j == 0 && ((c) >> 1) == 0) FP64EMU_COPY_A((kt) + kPF, ((c) & 1) * 2);                \
       if (j == 2 && ((c) >> 1) == 0) FP64EMU_COPY_A((kt) + kPF, ((c) & 1) * 2 + 1);            \
       if (j == 0 && ((c) >> 1) == 1) FP64EMU_COPY_B((kt) + kPF, ((c) & 1) * 2);                \
@@ -1734,8 +1729,8 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
         if ((c) == 3 && j == 3) {                                                            \
           _Pragma("unroll") for (int d_ = 0; d_ < 4; ++d_)                                   \
           _Pragma("unroll") for (int x_ = 0; x_ < 4; ++x_)                                   \
-            FP64EMU_XDOT(FC, kXon - 1 + x_, d_);                                             \
-          FP64EMU_READX((kt) + 1);                                                           \
+            FP64EMU_XDOT(FC, XR_##FC, kXon - 1 + x_, d_);                                    \
+          FP64EMU_XLOAD(XR_##FC, (kt) + 2);                                                  \
         }                                                                                    \
       }                                                                                      \
       __builtin_amdgcn_sched_barrier(0);                                                     \
@@ -1839,9 +1834,10 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     v4i F0[kWM + kWN], F1[kWM + kWN];                                                       \
     FP64EMU_READF(F0, (G0));                                                                \
     if constexpr (kXc > 0 && kXon > 0) {                                                    \
-      FP64EMU_READX((G0));                                                                  \
-      _Pragma("unroll") for (int x_ = 0; x_ < kWM; ++x_)                                    \
-      _Pragma("unroll") for (int ci_ = 0; ci_ < kXc; ++ci_) xacc[x_][ci_] = 0;              \
+      FP64EMU_XLOAD(XR_F0, (G0));                                                           \
+      FP64EMU_XLOAD(XR_F1, (G0) + 1);                                                       \
+      _Pragma("unroll") for (int x_ = 0; x_ < 4; ++x_)                                      \
+      _Pragma("unroll") for (int ci_ = 0; ci_ < kXc; ++ci_) xacc[kXon - 1 + x_][ci_] = 0;   \
     }                                                                                       \
     FP64EMU_RSTEP_R((G0), F0, F1, mma16_init);                                              \
     int kt_ = 1;                                                                            \
@@ -1980,8 +1976,6 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     int cleft = 0;
     const int8_t* nA = nullptr;
     const int8_t* nB = nullptr;
-    const int8_t* nX = nullptr;   // kXc: the extra columns' fragment (B's tile g.TN)
-    bool nXon = false;
     int64_t cend = e0 - (int64_t)cbl * g.nkt;               // stream end, from the piece's block
     auto copy_piece = [&](const int k) {
       const GemmItem t = stream_item(g, cbl * 32u + jl);
@@ -1991,10 +1985,6 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
       const int k0 = (ic ? t.slot * g.nkt : 0) + k;
       nA = g.A + t.b * g.memberA + (int64_t)pl * g.planeA + ((int64_t)t.mt * rs + k0) * kTileBytes;
       nB = g.B + t.b * g.memberB + (int64_t)pl * g.planeB + ((int64_t)t.nt * rs + k0) * kTileBytes;
-      if constexpr (kXc > 0) {
-        nXon = x_carrier(t.nt, (cbl * 32u + jl) / (uint32_t)(g.TM * g.TN));
-        nX = g.B + t.b * g.memberB + (int64_t)pl * g.planeB + ((int64_t)g.TN * rs + k0) * kTileBytes;
-      }
       cleft = (int)min<int64_t>(g.nkt, cend) - k;
     };
     copy_piece(kfirst);
@@ -2003,10 +1993,6 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
       cpB = nB;
       nA += kTileBytes;
       nB += kTileBytes;
-      if constexpr (kXc > 0) {
-        cpX = nXon ? nX : nullptr;
-        nX += kTileBytes;
-      }
       if (__builtin_expect(--cleft == 0, 0) && cend > g.nkt) {
         ++cbl;
         cend -= g.nkt;
@@ -2025,8 +2011,18 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     while (G0 < nk) {
       const int nj = min(g.nkt - k0, nk - G0);
       const GemmItem t = stream_item(g, bl * 32u + jl);
-      // A carrier of the extra columns: this wave's fragments 4 wn .. 4 wn + 3.
+      // A carrier of the extra columns: this wave's fragments 4 wn .. 4 wn + 3,
+      // their bytes from B's tile g.TN of the unit's plane at the piece's k.
       xon = kXc > 0 && x_carrier(t.nt, (bl * 32u + jl) / (uint32_t)(g.TM * g.TN));
+      if (kXc > 0 && xon) {
+        const bool ic = t.slot < g.ncorr;
+        const int pl = ic ? g.P : t.slot - g.ncorr;
+        const int rs = ic ? 2 * g.nkt : g.nkt;
+        const int kx = (ic ? t.slot * g.nkt : 0) + k0;
+        xsrc = g.B + t.b * g.memberB + (int64_t)pl * g.planeB + ((int64_t)g.TN * rs + kx) * kTileBytes;
+        xg0 = G0;
+        xg_last = G0 + nj - 1;
+      }
       if (kXc > 0 && xon && wn == 0) {
         constexpr int kXon = 1;
         FP64EMU_STREAM_SLOT(G0, nj);
@@ -2051,6 +2047,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
           for (int x_ = 0; x_ < kWM; ++x_)
 #pragma unroll
             for (int ci_ = 0; ci_ < kXc; ++ci_) {
+              if ((x_ >> 2) != wn) continue;   // the other wave's fragment
               int v = xacc[x_][ci_];
               v += __shfl_xor(v, 16);
               v += __shfl_xor(v, 32);
@@ -2271,8 +2268,7 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
 #undef FP64EMU_STREAM_SLOT
 #undef FP64EMU_COPY_A
 #undef FP64EMU_COPY_B
-#undef FP64EMU_COPY_X
-#undef FP64EMU_READX
+#undef FP64EMU_XLOAD
 #undef FP64EMU_XDOT
 #undef FP64EMU_SLOT
 
@@ -2422,13 +2418,11 @@ modgemm_split_kernel(GemmArgs g) {
 }
 
 // Split streams with kXc = g.xcols extra columns (a last tile column of at
-// most kXMax columns): the ring plus 1 KiB per stage for their B fragment.
+// most kXMax columns), computed beside the wide tiles.
 template <int kXc>
 __global__ void __launch_bounds__(kThreads, 1)
 modgemm_split_x_kernel(GemmArgs g) {
-  constexpr int kBytes = GemmShape<8, 8>::kLdsBytes + GemmShape<8, 8>::kS * 1024;
-  static_assert(kBytes <= 160 * 1024, "LDS ring and extra-column stages exceed the CU's 160 KiB");
-  __shared__ __attribute__((aligned(1024))) int8_t lds[kBytes];
+  __shared__ __attribute__((aligned(1024))) int8_t lds[GemmShape<8, 8>::kLdsBytes];
   modgemm_tile<false, 8, 8, false, true, true, kXc>(g, lds, GemmItem{});
 }
 
