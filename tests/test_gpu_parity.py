@@ -406,6 +406,11 @@ RUN_CASES = [
     ("mm", 1, 4096, 4096, 50, O.PRIMES[:2], True, None),               # 1, a run of two slots
     ("bmm", 256, 200, 200, 200, MODULI_ORDERS[1], True, None),         # 4, even modulus 254
     ("bmm_nt", 256, 240, 250, 64, O.PRIMES[:14], True, (256, 256)),   # 1, one tile per member
+    # Deeper slots (the c4 shape's 8 k-steps and more): streams of 9 to 32 k-steps per slot.
+    ("bmm_nt", 16, 1024, 1000, 1000, O.PRIMES[:14], True, (256, 256)),  # 16, ragged K and N
+    ("mm", 1, 4096, 4096, 520, O.PRIMES[:13], False, None),            # 9, no correction slot
+    ("bmm", 256, 200, 200, 700, MODULI_ORDERS[1], True, None),         # 11, even modulus 254
+    ("mm_nt", 1, 4096, 4096, 2048, O.PRIMES[:3], True, (256, 256)),    # 32, a run of three slots
 ]
 
 
@@ -440,6 +445,7 @@ THREE_RUN_CASES = [
     ("bmm", 270, 250, 250, 100, MODULI_ORDERS[1], True, 5),            # even modulus 254
     ("mm", 1, 4352, 4352, 100, O.PRIMES[:13], False, 5),               # 289 tiles: 5, 5, 3
     ("mm_nt", 1, 4200, 4500, 120, O.PRIMES[:20], True, 7),             # 306 tiles: 7, 7, 6
+    ("bmm_nt", 300, 240, 250, 512, O.PRIMES[:14], True, 5),            # 8 k-steps per slot
 ]
 
 
