@@ -2227,7 +2227,9 @@ __device__ __forceinline__ void modgemm_tile(const GemmArgs& g, int8_t* lds, con
     for (int s = 0; s < kPF; ++s)
       if (s < nk) FP64EMU_ISSUE(s);
     v4i F0[kWM + kWN], F1[kWM + kWN];
-    wait_vm_lgkm0<0>();
+    // Stage 0 landed (the copies of stages 1 and 2 may still be in flight:
+    // k-step 0 waits for stage 1 like every step).
+    if (nk >= kPF) wait_vm_lgkm0<(kPF - 1) * kDma>(); else wait_vm_lgkm0<0>();
     barrier_lds();
     FP64EMU_READF(F0, 0);
     // k-step 0 starts the accumulators; then pairs of steps alternate the
