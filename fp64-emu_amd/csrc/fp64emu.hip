@@ -521,8 +521,8 @@ void make_layout(int64_t batch, int64_t M, int64_t N, int64_t K, int P, bool cor
 // order (thread-strided partial sums, FMA accumulate, 256-wide tree), so the
 // Cauchy-Schwarz decision is reproducible by the CPU restatement.
 // fp64_emu_cuda/fp64_emu.cu:107-146.
-__device__ __forceinline__ float row_stats_out(double m, double s2, int bits, int16_t* sft,
-                                               float* lg) {
+__device__ __forceinline__ void row_stats_out(double m, double s2, int bits, int16_t* sft,
+                                              float* lg) {
   const int e = (m > 0.0 && isfinite(m)) ? ilogb(m) : 0;
   const int sh = (bits - 1) - e;
   float l;
@@ -530,23 +530,6 @@ __device__ __forceinline__ float row_stats_out(double m, double s2, int bits, in
   else l = (m > 0.0) ? INFINITY : -INFINITY;
   *lg = l;
   *sft = (int16_t)sh;
-  return l;
-}
-
-// The maximum of v over a block of T threads, stored by thread 0 to *dst
-// (every thread of the block calls it).
-template <int T>
-__device__ __forceinline__ void block_max_store(float v, float* dst) {
-  __shared__ float sm[T / 64];
-#pragma unroll
-  for (int s = 32; s > 0; s >>= 1) v = fmaxf(v, __shfl_xor(v, s));
-  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = v;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-#pragma unroll
-    for (int w = 1; w < T / 64; ++w) v = fmaxf(v, sm[w]);
-    *dst = v;
-  }
 }
 
 // One wave per row (four rows per block).  Lane l stands for the partial
@@ -575,7 +558,7 @@ __device__ __forceinline__ void row_pass(const double* __restrict__ x, int64_t c
 // block of kWaves waves holds kWaves / 4 such groups, or kWaves rows (one
 // per wave) otherwise.
 template <bool kGroup, int kWaves>
-__device__ __forceinline__ float size_rows_body(int64_t bid, const double* __restrict__ A, int64_t rowsA,
+__device__ __forceinline__ void size_rows_body(int64_t bid, const double* __restrict__ A, int64_t rowsA,
                                                const double* __restrict__ B, int64_t rows, int64_t K,
                                                int bits, int16_t* __restrict__ sftA,
                                                float* __restrict__ lgA, int16_t* __restrict__ sftB,
@@ -610,14 +593,14 @@ __device__ __forceinline__ float size_rows_body(int64_t bid, const double* __res
     sh_ss[wave][lane] = sw;
     sh_mx[wave][lane] = mw;
     __syncthreads();
-    if (wg != 0 || row >= rows) return -INFINITY;
+    if (wg != 0 || row >= rows) return;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       ss[u] = sh_ss[wave + u][lane];
       mx = fmax(mx, sh_mx[wave + u][lane]);
     }
   } else {
-    if (row >= rows) return -INFINITY;
+    if (row >= rows) return;
     // Sixteen loads in flight, then eight, then guarded 256-element blocks.
     int64_t c = 0;
     for (; c + 1024 <= K; c += 1024) row_pass<4>(x, c, mx, ss);
@@ -642,12 +625,10 @@ __device__ __forceinline__ float size_rows_body(int64_t bid, const double* __res
     t = t + __shfl_down(t, s);
     mx = fmax(mx, __shfl_down(mx, s));
   }
-  float l = -INFINITY;
   if (lane == 0) {
-    if (isA) l = row_stats_out(mx, t, bits, &sftA[r], &lgA[r]);
-    else l = row_stats_out(mx, t, bits, &sftB[r], &lgB[r]);
+    if (isA) row_stats_out(mx, t, bits, &sftA[r], &lgA[r]);
+    else row_stats_out(mx, t, bits, &sftB[r], &lgB[r]);
   }
-  return l;
 }
 
 template <bool kGroup>
@@ -695,10 +676,6 @@ void launch_size_rows(int64_t rows, hipStream_t s, const double* A, int64_t rows
 // ms, 4096^3 even), and on small products it saves the second launch
 // (128 x 128 x 4096 48.3 -> 46.2 us, 512^3 43.5 -> 38.8 us, 1000^3 70.9 ->
 // 66.3 us).
-// part != nullptr: every group also stores the maximum of its columns' or
-// rows' log2-norms, part[bid] for column group bid and part[partA + i] for row
-// group i, so that the width pick can read one value per group instead of
-// one per row and column (the pick inside the extraction).
 constexpr int kSizeThreads = 1024;
 constexpr int64_t kFusedSlabRows = 256;
 
@@ -708,12 +685,11 @@ size_rows_cols_kernel(const double* __restrict__ A, int64_t rowsA, int64_t ncolg
                       int16_t* __restrict__ sftA, float* __restrict__ lgA,
                       const double* __restrict__ X, int64_t totalcols, int64_t cols_per,
                       int64_t kslab, int nslab, int cpw, int16_t* __restrict__ sftB,
-                      float* __restrict__ lgB, float* __restrict__ part, int64_t partA) {
+                      float* __restrict__ lgB) {
   const int64_t bid = blockIdx.x;
   if (bid >= ncolgrp) {
-    const float l = size_rows_body<kGroup, kSizeThreads / 64>(bid - ncolgrp, A, rowsA, A, rowsA, K, bits,
-                                                              sftA, lgA, nullptr, nullptr);
-    if (part) block_max_store<kSizeThreads>(l, part + partA + (bid - ncolgrp));
+    size_rows_body<kGroup, kSizeThreads / 64>(bid - ncolgrp, A, rowsA, A, rowsA, K, bits, sftA, lgA,
+                                              nullptr, nullptr);
     return;
   }
   __shared__ double sh_m[kSizeThreads], sh_s[kSizeThreads];
@@ -747,31 +723,28 @@ size_rows_cols_kernel(const double* __restrict__ A, int64_t rowsA, int64_t ncolg
   sh_m[t] = mx;
   sh_s[t] = ss;
   __syncthreads();
-  float l = -INFINITY;
-  if (t < cpw && j < totalcols) {
-    // Slabs folded in order, sixteen LDS reads ahead of the adds.
-    double fm = 0.0, fs = 0.0;
-    int q = 0;
-    for (; q + 16 <= nslab; q += 16) {
-      double m[16], v[16];
+  if (t >= cpw || j >= totalcols) return;
+  // Slabs folded in order, sixteen LDS reads ahead of the adds.
+  double fm = 0.0, fs = 0.0;
+  int q = 0;
+  for (; q + 16 <= nslab; q += 16) {
+    double m[16], v[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        m[u] = sh_m[(q + u) * cpw + t];
-        v[u] = sh_s[(q + u) * cpw + t];
-      }
+    for (int u = 0; u < 16; ++u) {
+      m[u] = sh_m[(q + u) * cpw + t];
+      v[u] = sh_s[(q + u) * cpw + t];
+    }
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        fm = fmax(fm, m[u]);
-        fs = fs + v[u];
-      }
+    for (int u = 0; u < 16; ++u) {
+      fm = fmax(fm, m[u]);
+      fs = fs + v[u];
     }
-    for (; q < nslab; ++q) {
-      fm = fmax(fm, sh_m[q * cpw + t]);
-      fs = fs + sh_s[q * cpw + t];
-    }
-    l = row_stats_out(fm, fs, bits, &sftB[j], &lgB[j]);
   }
-  if (part) block_max_store<kSizeThreads>(l, part + bid);
+  for (; q < nslab; ++q) {
+    fm = fmax(fm, sh_m[q * cpw + t]);
+    fs = fs + sh_s[q * cpw + t];
+  }
+  row_stats_out(fm, fs, bits, &sftB[j], &lgB[j]);
 }
 
 // Column partials of a [K, N] operand (per batch member): thread j owns
@@ -981,9 +954,6 @@ pick_width_kernel(const float* __restrict__ lgA, int64_t m, const float* __restr
 // 64.7 -> 62.6 us (mm); up to kPickInExtractBytes of those reads over the
 // launch (2048^3: 32 MiB, still 3% faster); past it the reads cost more
 // than the launch (1023 x 2049 x 32769: 295 MiB, 1.609 against 1.620 ms).
-// Larger products sized by the single column-sizing launch read its one
-// maximum per work group instead (size_rows_cols_kernel's part), under the
-// same bound on the bytes the extraction groups read.
 constexpr int64_t kPickInExtractMax = 4096;
 constexpr int64_t kPickInExtractBytes = 64ll << 20;
 
@@ -3456,18 +3426,7 @@ int run(const Call& c) {
       if (gsz > limit) return fail(FP64EMU_EINVAL, "problem too large for one launch");
   }
 
-  // 1. sizing, then the width pick: its own launch, or inside the extraction
-  // (every extraction group reduces the log2-norms itself) when the values it
-  // reads stay small: all rows' and columns' (pick_small), or the fused
-  // sizing launch's one maximum per group (use_part, stored in pss, which that
-  // launch does not use otherwise).
-  const float log2M = std::min(tab.log2M, 126.0f);
-  const int64_t ext_groups = c.batch * (L.ext_rowsA / 64 + L.ext_rowsB / 64) * (L.Kp / kTileK);
-  const bool pick_small = L.nchunk == 1 && L.nseg == 1 && MF + NF <= kPickInExtractMax &&
-                          (MF + NF) * (int64_t)sizeof(float) * ext_groups <= kPickInExtractBytes;
-  bool use_part = false;
-  float* part = reinterpret_cast<float*>(pss);
-  int64_t part_a = 0, part_na = 0, part_nb = 0;   // A's maxima at part + part_a
+  // 1. sizing
   if (!c.b_kn) {
     launch_size_rows(MF + NF, s, c.A, MF, c.B, c.K, c.bits, sftA, lgA, sftB, lgB);
   } else {
@@ -3481,22 +3440,12 @@ int run(const Call& c) {
       const int64_t nrow = group ? (MF + kSizeThreads / 256 - 1) / (kSizeThreads / 256)
                                  : (MF + kSizeThreads / 64 - 1) / (kSizeThreads / 64);
       const unsigned grid = (unsigned)(nrow + ncolgrp);
-      part_a = (ncolgrp + 3) / 4 * 4;   // 16-byte aligned, for the pick's vector reads
-      part_na = nrow;
-      part_nb = ncolgrp;
-      const int64_t part_bytes = (part_a + nrow) * (int64_t)sizeof(float);
-      use_part = !pick_small && L.nchunk == 1 && L.nseg == 1 &&
-                 part_bytes <= (int64_t)sizeof(double) * nslab * NF &&
-                 part_bytes * ext_groups <= kPickInExtractBytes;
-      float* pp = use_part ? part : nullptr;
       if (group)
         hipLaunchKernelGGL(size_rows_cols_kernel<true>, dim3(grid), dim3(kSizeThreads), 0, s, c.A, MF,
-                           ncolgrp, c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, nslab, cpw, sftB, lgB,
-                           pp, part_a);
+                           ncolgrp, c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, nslab, cpw, sftB, lgB);
       else
         hipLaunchKernelGGL(size_rows_cols_kernel<false>, dim3(grid), dim3(kSizeThreads), 0, s, c.A, MF,
-                           ncolgrp, c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, nslab, cpw, sftB, lgB,
-                           pp, part_a);
+                           ncolgrp, c.K, c.bits, sftA, lgA, c.B, NF, c.N, kslab, nslab, cpw, sftB, lgB);
     } else {
       const int64_t gcx = (NF + kThreads - 1) / kThreads;
       const int64_t nrow = group ? MF : (MF + kRowsPerBlock - 1) / kRowsPerBlock;
@@ -3512,7 +3461,10 @@ int run(const Call& c) {
                          dim3(kThreads), 0, s, pmax, pss, NF, nslab, c.bits, sftB, lgB);
     }
   }
-  const bool pick_in_extract = pick_small || use_part;
+  const float log2M = std::min(tab.log2M, 126.0f);
+  const int64_t ext_groups = c.batch * (L.ext_rowsA / 64 + L.ext_rowsB / 64) * (L.Kp / kTileK);
+  const bool pick_in_extract = L.nchunk == 1 && L.nseg == 1 && MF + NF <= kPickInExtractMax &&
+                               (MF + NF) * (int64_t)sizeof(float) * ext_groups <= kPickInExtractBytes;
   if (!pick_in_extract)
     hipLaunchKernelGGL(pick_width_kernel, dim3(1), dim3(kPickThreads), 0, s, lgA, MF, lgB, NF, log2M,
                        c.bits, bits_eff);
@@ -3547,12 +3499,7 @@ int run(const Call& c) {
       ea.div_rg[3] = make_fastdiv(ea.rgB - ea.rgB_data);
       ea.sftA = sftA + m0; ea.sftB = sftB; ea.bits_eff = bits_eff;
       ea.pick = pick_in_extract ? 1 : 0; ea.bits = c.bits; ea.log2M = log2M;
-      if (use_part) {
-        ea.lgA = part + part_a; ea.lgB = part; ea.nlgA = part_na; ea.nlgB = part_nb;
-      } else {
-        ea.lgA = lgA; ea.lgB = lgB; ea.nlgA = MF; ea.nlgB = NF;
-      }
-      ea.bits_out = bits_eff;
+      ea.lgA = lgA; ea.lgB = lgB; ea.nlgA = MF; ea.nlgB = NF; ea.bits_out = bits_eff;
       ea.planesA = planesA; ea.planesB = planesB;
       ea.P = c.P;
       const int64_t wg = c.batch * (ea.rgA + ea.rgB) * nkt;
